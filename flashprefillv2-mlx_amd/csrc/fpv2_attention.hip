@@ -1,0 +1,530 @@
+// Block-sparse FlashAttention-2 forward with pooled mean correction, gfx950.
+//
+// Semantics follow the fpv2_sparse_attention Metal kernel
+// (fpv2/kernel.py:187-414): for each query row, an online base-2 softmax over
+// the keys of the tile's selected blocks (ascending list, stop at the first
+// block past the tile's last row, causal mask on the diagonal), then — with
+// mean correction — over the pooled K/V rows of the tile's pruned blocks with
+// a +log2(block_k) logit shift; O /= l at the end.
+//
+// MI355X mapping:
+//   * one workgroup = one (KV head, query tile, 128-row chunk); the tile's
+//     G*tile_q packed rows (row = g*tile_q + p) share the block lists, so the
+//     G query heads of a KV head share every K/V load (the hook's tile is
+//     128 packed rows: one chunk);
+//   * 4 waves x 32 rows; Q lives in VGPRs for the whole workgroup;
+//   * S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: lane l owns query
+//     row l%32 and 16 of the 32 keys of each key tile, so row max/sum need a
+//     single lane-pair exchange and P feeds the next MFMA without a transpose;
+//   * O^T = V^T . P^T: the rescale by exp2(m_old - m_new) is lane-local;
+//   * K/V sub-tiles of 64 keys are double-buffered in LDS: the next sub-tile's
+//     global loads are in flight while the current one is multiplied; V is
+//     transposed on its way into LDS so both MFMA operands are 8-byte/16-byte
+//     LDS reads; row strides are padded against bank conflicts;
+//   * grid order puts the KV head in the low bits of the workgroup id, so the
+//     round-robin dispatch over the 8 XCDs keeps one head per XCD L2 (for
+//     Hkv = 8), and tiles run latest (longest) first.
+#include "fpv2_common.h"
+
+namespace fpv2 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;  // packed query rows per workgroup
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* pk;
+  const uint16_t* pv;
+  const int32_t* ids;
+  const int32_t* counts;
+  const int32_t* pids;
+  const int32_t* pcounts;
+  uint16_t* out;
+  int G, Hkv, Nt, Nb, Lq, out_rows, Lk, offset, bk, tq, nchunk;
+  float c_scale;  // scale * log2(e)
+  float shift;    // log2(block_k)
+  int64_t q_hs, k_hs, v_hs, o_hs, o_rs;
+  int q_rs, k_rs, v_rs;
+  uint32_t q_bytes, k_bytes, v_bytes, pooled_bytes;  // descriptor ranges
+};
+
+enum Phase { kSel = 0, kCorr = 1, kDone = 2 };
+
+struct Step {
+  int phase;
+  int li;     // list index (selected phase) / first list entry (correction)
+  int sub;    // sub-tile within the block (selected phase)
+  int key0;   // first key of the sub-tile (selected phase)
+  int nkeys;  // valid keys in the sub-tile (selected) / entries (correction)
+};
+
+__device__ __forceinline__ int clampi(int x, int lo, int hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// Keys per LDS sub-tile: 64 where the registers allow it, 32 for wide heads.
+template <int D> struct SubTile { static constexpr int BN = D <= 64 ? 64 : 32; };
+
+template <typename T, int D, bool CORR>
+struct AttnTile {
+  static constexpr int BN = SubTile<D>::BN;     // keys per sub-tile
+  static constexpr int LDV = BN + 4;            // V^T row stride (elements)
+  static constexpr int LDK = D + 8;             // K row stride (elements)
+  static constexpr int KS = D / 16;             // QK^T k-steps
+  static constexpr int DT = D / 32;             // O^T row tiles (32 dims)
+  static constexpr int NTK = BN / 32;           // S^T key tiles
+  static constexpr int DG = D / 8;              // 8-dim groups
+  static constexpr int KCHUNKS = BN * DG;       // 16-B K chunks per sub-tile
+  static constexpr int KTASK = (KCHUNKS + kThreads - 1) / kThreads;
+  static constexpr int DGP = (DG + 7) / 8 * 8;  // padded to whole 8-lane groups
+  static constexpr int VTASKS = (BN / 4) * DGP;
+  static constexpr int VT = (VTASKS + kThreads - 1) / kThreads;
+  static constexpr int K_ELEMS = BN * LDK;
+  static constexpr int V_ELEMS = D * LDV;
+  static constexpr int STAGE = K_ELEMS + V_ELEMS;  // uint16 elements per stage
+};
+
+template <typename T, int D, bool CORR>
+__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
+  using TL = AttnTile<T, D, CORR>;
+  using vec8 = typename Elem<T>::vec8;
+  constexpr int BN = TL::BN;
+  constexpr int LDV = TL::LDV;
+  extern __shared__ __align__(16) uint16_t lds[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hf = lane >> 5;
+
+  // ---- workgroup -> (KV head, tile, row chunk); latest tiles first ----
+  const int bid = blockIdx.x;
+  const int h = bid % a.Hkv;
+  const int rest = bid / a.Hkv;
+  const int chunk = rest % a.nchunk;
+  const int t = a.Nt - 1 - rest / a.nchunk;
+  const int abs_first = a.offset + t * a.tq;
+  const int last_local = min((t + 1) * a.tq, a.Lq);
+  const int abs_last = a.offset + last_local - 1;
+
+  // ---- this lane's query row ----
+  const int R = a.G * a.tq;
+  const int prow = chunk * kRows + wave * 32 + l32;
+  const bool exists = prow < R;
+  int g = 0, pos = 0;
+  if (exists) {
+    g = prow / a.tq;
+    pos = t * a.tq + (prow - g * a.tq);
+  }
+  const bool row_valid = exists && pos < a.Lq;
+  const int qpos_abs = a.offset + pos;
+
+  vec8 qf[TL::KS];
+  {
+    const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
+    const uint32_t qoff =
+        row_valid ? static_cast<uint32_t>((g * a.q_hs + static_cast<int64_t>(pos) * a.q_rs + hf * 8) * 2)
+                  : kOOB;
+#pragma unroll
+    for (int k = 0; k < TL::KS; ++k) qf[k] = as_vec8<T>(buf_load16(qr, qoff + (row_valid ? k * 32 : 0)));
+  }
+
+  // ---- block lists of (h, t), clipped as kernel.py:555-558 ----
+  const int Nb = a.Nb;
+  const int64_t list_row = static_cast<int64_t>(h) * a.Nt + t;
+  const int32_t* ids = a.ids + list_row * Nb;
+  const int32_t* pids = a.pids + list_row * Nb;
+  const int sel_count = clampi(a.counts[list_row], 0, Nb);
+  const int pr_count = CORR ? clampi(a.pcounts[list_row], 0, Nb) : 0;
+  const int subs = (a.bk + BN - 1) / BN;
+
+  auto make_sel = [&](int li, int sub) -> Step {
+    const int blk = clampi(ids[li], 0, Nb - 1);
+    Step s;
+    s.phase = kSel;
+    s.li = li;
+    s.sub = sub;
+    s.key0 = blk * a.bk + sub * BN;
+    const int n = min(min(a.bk - sub * BN, BN), a.Lk - s.key0);
+    s.nkeys = n < 0 ? 0 : n;
+    return s;
+  };
+  auto corr_start = [&]() -> Step {
+    Step s{kDone, 0, 0, 0, 0};
+    if (CORR && pr_count > 0) {
+      s.phase = kCorr;
+      s.nkeys = min(pr_count, BN);
+    }
+    return s;
+  };
+  auto first_step = [&]() -> Step {
+    if (sel_count > 0) {
+      const Step s = make_sel(0, 0);
+      if (s.key0 <= abs_last) return s;
+    }
+    return corr_start();
+  };
+  auto advance = [&](const Step& c) -> Step {
+    if (c.phase == kSel) {
+      if (c.sub + 1 < subs) {
+        const Step s = make_sel(c.li, c.sub + 1);
+        if (s.key0 <= abs_last) return s;
+      }
+      if (c.li + 1 < sel_count) {
+        const Step s = make_sel(c.li + 1, 0);
+        if (s.key0 <= abs_last) return s;
+      }
+      return corr_start();
+    }
+    if (c.phase == kCorr && c.li + BN < pr_count) {
+      Step s{kCorr, c.li + BN, 0, 0, min(pr_count - c.li - BN, BN)};
+      return s;
+    }
+    Step d{kDone, 0, 0, 0, 0};
+    return d;
+  };
+
+  // ---- global -> register staging of one sub-tile (buffer loads) ----
+  const rsrc_t kr = make_rsrc(a.k + h * a.k_hs, a.k_bytes);
+  const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
+  const rsrc_t pkr = make_rsrc(a.pk + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
+  const rsrc_t pvr = make_rsrc(a.pv + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
+  u32x4 kreg[TL::KTASK];
+  u32x4 vreg[TL::VT][4];
+
+  auto load_step = [&](const Step& s) {
+    if (s.phase == kSel) {
+#pragma unroll
+      for (int i = 0; i < TL::KTASK; ++i) {
+        const int tau = tid + i * kThreads;
+        const int e = tau / TL::DG;
+        const int c = tau - e * TL::DG;
+        const uint32_t off = (tau < TL::KCHUNKS && e < s.nkeys)
+                                 ? static_cast<uint32_t>(((s.key0 + e) * a.k_rs + c * 8) * 2)
+                                 : kOOB;
+        kreg[i] = buf_load16(kr, off);
+      }
+#pragma unroll
+      for (int i = 0; i < TL::VT; ++i) {
+        const int tau = tid + i * kThreads;
+        const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
+        const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
+        const bool task_ok = tau < TL::VTASKS && dg < TL::DG;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int e = kg * 4 + r;
+          const uint32_t off = (task_ok && e < s.nkeys)
+                                   ? static_cast<uint32_t>(((s.key0 + e) * a.v_rs + dg * 8) * 2)
+                                   : kOOB;
+          vreg[i][r] = buf_load16(vr, off);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TL::KTASK; ++i) {
+        const int tau = tid + i * kThreads;
+        const int e = tau / TL::DG;
+        const int c = tau - e * TL::DG;
+        const bool ok = tau < TL::KCHUNKS && e < s.nkeys;
+        const int blk = clampi(pids[ok ? s.li + e : s.li], 0, Nb - 1);
+        const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
+        kreg[i] = buf_load16(pkr, off);
+      }
+#pragma unroll
+      for (int i = 0; i < TL::VT; ++i) {
+        const int tau = tid + i * kThreads;
+        const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
+        const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
+        const bool task_ok = tau < TL::VTASKS && dg < TL::DG;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int e = kg * 4 + r;
+          const bool ok = task_ok && e < s.nkeys;
+          const int blk = clampi(pids[ok ? s.li + e : s.li], 0, Nb - 1);
+          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + dg * 8) * 2) : kOOB;
+          vreg[i][r] = buf_load16(pvr, off);
+        }
+      }
+    }
+  };
+
+  auto store_step = [&](int buf) {
+    uint16_t* ks = lds + buf * TL::STAGE;
+    uint16_t* vs = ks + TL::K_ELEMS;
+#pragma unroll
+    for (int i = 0; i < TL::KTASK; ++i) {
+      const int tau = tid + i * kThreads;
+      const int e = tau / TL::DG;
+      const int c = tau - e * TL::DG;
+      if (tau < TL::KCHUNKS) store16(ks + e * TL::LDK + c * 8, kreg[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < TL::VT; ++i) {
+      const int tau = tid + i * kThreads;
+      const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
+      const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
+      if (tau < TL::VTASKS && dg < TL::DG) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {  // dims 8dg + 2w, 8dg + 2w + 1
+          const uint32_t r0 = vreg[i][0][w], r1 = vreg[i][1][w];
+          const uint32_t r2 = vreg[i][2][w], r3 = vreg[i][3][w];
+          u32x2 lo, hi;
+          lo[0] = (r0 & 0xffffu) | (r1 << 16);
+          lo[1] = (r2 & 0xffffu) | (r3 << 16);
+          hi[0] = (r0 >> 16) | (r1 & 0xffff0000u);
+          hi[1] = (r2 >> 16) | (r3 & 0xffff0000u);
+          const int d = dg * 8 + 2 * w;
+          *reinterpret_cast<u32x2*>(vs + d * LDV + kg * 4) = lo;
+          *reinterpret_cast<u32x2*>(vs + (d + 1) * LDV + kg * 4) = hi;
+        }
+      }
+    }
+  };
+
+  // ---- accumulators ----
+  f32x16 o[TL::DT];
+#pragma unroll
+  for (int i = 0; i < TL::DT; ++i) o[i] = f32x16{};
+  float m_run = neg_inf();
+  float l_run = 0.f;
+
+  auto compute_step = [&](const Step& s, int buf) {
+    const uint16_t* ks = lds + buf * TL::STAGE;
+    const uint16_t* vs = ks + TL::K_ELEMS;
+    f32x16 st[TL::NTK];
+#pragma unroll
+    for (int kt = 0; kt < TL::NTK; ++kt) {
+      st[kt] = f32x16{};
+#pragma unroll
+      for (int k = 0; k < TL::KS; ++k) {
+        const u32x4 kv = load16(ks + (kt * 32 + l32) * TL::LDK + k * 16 + hf * 8);
+        st[kt] = Elem<T>::mfma32(as_vec8<T>(kv), qf[k], st[kt]);
+      }
+    }
+    // scale to log2 units, shift pooled entries, mask
+    const bool sel = s.phase == kSel;
+    const float shift = sel ? 0.f : a.shift;
+    const bool need_mask = (s.nkeys < BN) || (sel && s.key0 + BN - 1 > abs_first);
+    const int key_lim = sel ? qpos_abs - s.key0 : BN;  // causal: e <= key_lim
+    float mx = neg_inf();
+#pragma unroll
+    for (int kt = 0; kt < TL::NTK; ++kt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float x = st[kt][j] * a.c_scale + shift;
+        if (need_mask) {
+          const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
+          x = (e < s.nkeys && e <= key_lim) ? x : neg_inf();
+        }
+        st[kt][j] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == neg_inf()) ? 0.f : m_new;
+    const float rescale = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float lsum = 0.f;
+    vec8 pb[TL::NTK][2];
+#pragma unroll
+    for (int kt = 0; kt < TL::NTK; ++kt) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = __builtin_amdgcn_exp2f(st[kt][u * 8 + 2 * i] - m_use);
+          const float p1 = __builtin_amdgcn_exp2f(st[kt][u * 8 + 2 * i + 1] - m_use);
+          lsum += p0 + p1;
+          w[i] = pack2<T>(p0, p1);
+        }
+        pb[kt][u] = as_vec8<T>(w);
+      }
+    }
+    l_run = l_run * rescale + lsum;
+#pragma unroll
+    for (int dt = 0; dt < TL::DT; ++dt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) o[dt][j] *= rescale;
+    }
+    // O^T += V^T . P^T
+#pragma unroll
+    for (int dt = 0; dt < TL::DT; ++dt) {
+      const uint16_t* vrow = vs + (dt * 32 + l32) * LDV + hf * 4;
+#pragma unroll
+      for (int kt = 0; kt < TL::NTK; ++kt) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const u32x2 x0 = *reinterpret_cast<const u32x2*>(vrow + kt * 32 + u * 16);
+          const u32x2 x1 = *reinterpret_cast<const u32x2*>(vrow + kt * 32 + u * 16 + 8);
+          const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
+          o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[kt][u], o[dt]);
+        }
+      }
+    }
+  };
+
+  // ---- pipelined loop over sub-tiles ----
+  Step cur = first_step();
+  if (cur.phase != kDone) {
+    load_step(cur);
+    store_step(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  while (cur.phase != kDone) {
+    const Step nxt = advance(cur);
+    if (nxt.phase != kDone) load_step(nxt);
+    compute_step(cur, buf);
+    if (nxt.phase != kDone) store_step(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    cur = nxt;
+  }
+
+  // ---- normalise and store ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  if (!exists || pos >= a.out_rows) return;
+  const float inv = (row_valid && l_tot > 0.f) ? 1.f / l_tot : 0.f;
+  uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g) * a.o_hs + pos * a.o_rs;
+#pragma unroll
+  for (int dt = 0; dt < TL::DT; ++dt) {
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const int d0 = dt * 32 + jg * 8 + hf * 4;
+      u32x2 w;
+      w[0] = pack2<T>(o[dt][jg * 4 + 0] * inv, o[dt][jg * 4 + 1] * inv);
+      w[1] = pack2<T>(o[dt][jg * 4 + 2] * inv, o[dt][jg * 4 + 3] * inv);
+      *reinterpret_cast<u32x2*>(orow + d0) = w;
+    }
+  }
+}
+
+template <typename T, int D, bool CORR>
+int launch_attn(const AttnArgs& a, hipStream_t stream) {
+  using TL = AttnTile<T, D, CORR>;
+  const size_t lds = 2 * TL::STAGE * sizeof(uint16_t);
+  auto kernel = sparse_attn_kernel<T, D, CORR>;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return fail(FPV2_ERR_LAUNCH, "sparse_attention: hipFuncSetAttribute failed");
+  const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
+  if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), lds, stream, a);
+  return check_launch("sparse_attention");
+}
+
+template <typename T>
+int dispatch_attn(int64_t D, bool corr, const AttnArgs& a, hipStream_t s) {
+  switch (D) {
+    case 64: return corr ? launch_attn<T, 64, true>(a, s) : launch_attn<T, 64, false>(a, s);
+    case 96: return corr ? launch_attn<T, 96, true>(a, s) : launch_attn<T, 96, false>(a, s);
+    case 128: return corr ? launch_attn<T, 128, true>(a, s) : launch_attn<T, 128, false>(a, s);
+    case 256: return corr ? launch_attn<T, 256, true>(a, s) : launch_attn<T, 256, false>(a, s);
+    default:
+      return fail(FPV2_ERR_UNSUPPORTED, "head dimension must be one of (64, 96, 128, 256)");
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+}  // namespace fpv2
+
+extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v,
+                                     const void* pooled_k, const void* pooled_v,
+                                     const int32_t* selected_ids, const int32_t* selected_counts,
+                                     const int32_t* pruned_ids, const int32_t* pruned_counts,
+                                     void* out, int dtype, const fpv2_attn_params* p,
+                                     void* stream) {
+  using namespace fpv2;
+  if (!p || !q || !k || !v || !pooled_k || !pooled_v || !selected_ids || !selected_counts ||
+      !pruned_ids || !pruned_counts || !out)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention: null argument");
+  if (dtype != FPV2_BF16 && dtype != FPV2_F16)
+    return fail(FPV2_ERR_UNSUPPORTED, "q, k, and v must share float16 or bfloat16 dtype");
+  if (p->kv_heads <= 0 || p->query_heads <= 0 || p->query_heads % p->kv_heads)
+    return fail(FPV2_ERR_ARGUMENT, "query heads must be divisible by KV heads");
+  if (p->block_k <= 0 || p->tile_q <= 0 || p->num_blocks <= 0)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention: block_k, tile_q and num_blocks must be positive");
+  if (p->padded_query_length <= 0 || p->padded_query_length % p->tile_q)
+    return fail(FPV2_ERR_ARGUMENT, "q and k/v sequence lengths must be tile/block aligned");
+  if (p->query_length <= 0 || p->query_length > p->padded_query_length)
+    return fail(FPV2_ERR_ARGUMENT, "query_length must fit within padded q");
+  if (p->out_rows < p->query_length || p->out_rows > p->padded_query_length)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention: out_rows must lie in [query_length, padded]");
+  if (p->key_length <= 0 || p->key_length > p->num_blocks * p->block_k)
+    return fail(FPV2_ERR_ARGUMENT, "key_length must fit within padded k/v");
+  if (p->offset < 0 || p->offset + p->query_length > p->key_length)
+    return fail(FPV2_ERR_ARGUMENT, "offset does not align queries within the key sequence");
+  const int64_t strides[8] = {p->q_head_stride, p->q_row_stride, p->k_head_stride,
+                              p->k_row_stride, p->v_head_stride, p->v_row_stride,
+                              p->o_head_stride, p->o_row_stride};
+  for (int i = 0; i < 8; ++i)
+    if (strides[i] % 8) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: strides must be multiples of 8 elements");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(pooled_k) ||
+      !aligned16(pooled_v) || reinterpret_cast<uintptr_t>(out) % 8)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: tensors must be 16-byte aligned");
+  const int64_t G = p->query_heads / p->kv_heads;
+  const int64_t D = p->head_dim;
+  const int64_t Nt = p->padded_query_length / p->tile_q;
+  const int64_t q_bytes = ((G - 1) * p->q_head_stride + (p->query_length - 1) * p->q_row_stride + D) * 2;
+  const int64_t k_bytes = ((p->key_length - 1) * p->k_row_stride + D) * 2;
+  const int64_t v_bytes = ((p->key_length - 1) * p->v_row_stride + D) * 2;
+  const int64_t pooled_bytes = p->num_blocks * D * 2;
+  if (q_bytes > kMaxRsrcBytes || k_bytes > kMaxRsrcBytes || v_bytes > kMaxRsrcBytes ||
+      pooled_bytes > kMaxRsrcBytes)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: a head group spans more than 2 GiB");
+  if (p->q_row_stride < D || p->k_row_stride < D || p->v_row_stride < D || p->o_row_stride < D)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention: row strides must be >= head_dim");
+  if (p->kv_heads * Nt * ((G * p->tile_q + kRows - 1) / kRows) > 0x7fffffffLL ||
+      p->num_blocks * p->block_k > 0x7fffffffLL || G * p->tile_q > 0x7fffffffLL ||
+      p->padded_query_length > 0x7fffffffLL)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: sizes exceed 32-bit indexing");
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.pk = static_cast<const uint16_t*>(pooled_k);
+  a.pv = static_cast<const uint16_t*>(pooled_v);
+  a.ids = selected_ids;
+  a.counts = selected_counts;
+  a.pids = pruned_ids;
+  a.pcounts = pruned_counts;
+  a.out = static_cast<uint16_t*>(out);
+  a.Hkv = static_cast<int>(p->kv_heads);
+  a.G = static_cast<int>(G);
+  a.Nt = static_cast<int>(Nt);
+  a.Nb = static_cast<int>(p->num_blocks);
+  a.Lq = static_cast<int>(p->query_length);
+  a.out_rows = static_cast<int>(p->out_rows);
+  a.Lk = static_cast<int>(p->key_length);
+  a.offset = static_cast<int>(p->offset);
+  a.bk = static_cast<int>(p->block_k);
+  a.tq = static_cast<int>(p->tile_q);
+  a.nchunk = static_cast<int>((G * p->tile_q + kRows - 1) / kRows);
+  a.c_scale = static_cast<float>(p->scale * 1.4426950408889634);
+  a.shift = static_cast<float>(__builtin_log2(static_cast<double>(p->block_k)));
+  a.q_hs = p->q_head_stride;
+  a.k_hs = p->k_head_stride;
+  a.v_hs = p->v_head_stride;
+  a.o_hs = p->o_head_stride;
+  a.o_rs = p->o_row_stride;
+  a.q_rs = static_cast<int>(p->q_row_stride);
+  a.k_rs = static_cast<int>(p->k_row_stride);
+  a.v_rs = static_cast<int>(p->v_row_stride);
+  a.q_bytes = static_cast<uint32_t>(q_bytes);
+  a.k_bytes = static_cast<uint32_t>(k_bytes);
+  a.v_bytes = static_cast<uint32_t>(v_bytes);
+  a.pooled_bytes = static_cast<uint32_t>(pooled_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool corr = p->mean_correction != 0;
+  return dtype == FPV2_BF16 ? dispatch_attn<bf16_t>(p->head_dim, corr, a, s)
+                            : dispatch_attn<f16_t>(p->head_dim, corr, a, s);
+}

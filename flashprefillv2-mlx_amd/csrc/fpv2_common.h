@@ -1,0 +1,125 @@
+// Shared device/host helpers for the gfx950 FPV2 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fpv2.h"
+
+namespace fpv2 {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (thread-local message behind fpv2_last_error).
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int status, const char* fmt, ...);
+int check_launch(const char* kernel);
+
+// ---------------------------------------------------------------------------
+// Vector types.  16-bit element types are carried as raw uint16 bits in
+// memory; the MFMA operands are 8-element vectors of the element type.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+// Element traits: memory type, MFMA operand type and conversions.
+template <typename T> struct Elem;
+
+template <> struct Elem<bf16_t> {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_float(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  }
+  // float -> bf16, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+  static __device__ __forceinline__ uint16_t from_float(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<f16_t> {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_float(uint16_t b) {
+    _Float16 h = __builtin_bit_cast(_Float16, b);
+    return static_cast<float>(h);
+  }
+  static __device__ __forceinline__ uint16_t from_float(float f) {
+    _Float16 h = static_cast<_Float16>(f);  // round-to-nearest-even
+    return __builtin_bit_cast(uint16_t, h);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Pack two floats into two 16-bit elements of T (low half = a), RNE.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<bf16_t>(float a, float b) {
+  const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
+  const f16x2 v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 v) {
+  return __builtin_bit_cast(typename Elem<T>::vec8, v);
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void store16(void* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+
+// Raw buffer access.  A resource descriptor covers [base, base + bytes);
+// loads at offsets past the range return zeros (hardware range check), so
+// masked rows are read branch-free with offset kOOB.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // gfx9-family raw buffer format
+constexpr uint32_t kOOB = 0x80000000u;        // any offset >= range reads 0
+constexpr int64_t kMaxRsrcBytes = 0x7fffffffLL;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), static_cast<int>(kRsrcWord3));
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// Correct rounding of a double to the 16-bit formats: round to float with
+// round-to-odd (sticky bit), then round-to-nearest-even to 16 bits.  The
+// double -> float step keeps 13+ guard bits, so the result equals a single
+// rounding of the double.
+__device__ __forceinline__ float double_to_float_odd(double x) {
+  float f = static_cast<float>(x);  // round-to-nearest-even
+  double fd = static_cast<double>(f);
+  if (__builtin_fabs(fd) > __builtin_fabs(x)) {
+    f = __uint_as_float(__float_as_uint(f) - 1u);  // one step toward zero
+    fd = static_cast<double>(f);
+  }
+  if (fd != x && __builtin_isfinite(x)) f = __uint_as_float(__float_as_uint(f) | 1u);
+  return f;
+}
+
+}  // namespace fpv2

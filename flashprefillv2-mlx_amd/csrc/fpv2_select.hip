@@ -1,0 +1,585 @@
+// Pooled-QK scoring, block selection and list compaction.
+//
+// Restates fpv2/selection.py:109-201 (block_scores_and_select) fused with
+// fpv2/kernel.py:141-184 (compact_block_indices).  One workgroup owns one
+// (KV head h, query tile t): the tile's G*tile_q packed query rows (head-major:
+// row = g*tile_q + p) are scored against the pooled keys with bf16/f16 MFMA
+// (S = Q . Kbar^T, fp32 accumulation), each block's energy
+//     E_b = sum_{g,rows} exp(s - m),  m = max over fully visible blocks
+// is reduced on the fly as (c_b, e_b) = (column max, sum exp(s - c_b)) so
+// no [rows, Nb] score tile is ever materialised, then
+//     selected = (E_b >= alpha * max_b E_b | sink | local | dense tail) & visible
+// and the mask is compacted in LDS into the fixed-width ascending lists
+// (selected ascending, then the rest ascending — a stable argsort of -mask),
+// with no host synchronisation.
+#include "fpv2_common.h"
+
+namespace fpv2 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRowsPerPass = 128;  // 4 waves x 32 rows
+
+struct SelectArgs {
+  const void* q;
+  const void* pk;
+  int64_t G, Hkv, Nt, Nb, Lq_pad, Lq, Lk, offset, bk, tq, sink, window, last_n;
+  float scale, alpha;
+  int64_t q_hs, q_rs;
+  uint8_t* sel_out;
+  float* scores;
+  int32_t* ids;
+  int32_t* counts;
+  int32_t* pids;
+  int32_t* pcounts;
+};
+
+struct TileInfo {
+  int64_t h, t, tile_first, tile_last, nfv, nvis;
+};
+
+__device__ __forceinline__ TileInfo tile_info(const SelectArgs& a) {
+  TileInfo ti;
+  const int64_t bid = blockIdx.x;
+  ti.h = bid % a.Hkv;
+  ti.t = a.Nt - 1 - bid / a.Hkv;  // latest tiles (longest rows) first
+  ti.tile_first = a.offset + ti.t * a.tq;
+  int64_t last = ti.tile_first + a.tq;
+  if (last > a.offset + a.Lq) last = a.offset + a.Lq;
+  ti.tile_last = last - 1;
+  int64_t nfv = (ti.tile_last + 1) / a.bk;  // blocks with end <= tile_last + 1
+  if (nfv > a.Nb) nfv = a.Nb;
+  if (nfv < 0) nfv = 0;
+  ti.nfv = nfv;
+  return ti;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Block-wide max (all threads get the result).  `red` holds >= 4 floats.
+__device__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return r;
+}
+__device__ int block_sum_int(int v, int* red) {
+  v = wave_sum_int(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  int r = red[0] + red[1] + red[2] + red[3];
+  __syncthreads();
+  return r;
+}
+
+// Merge (c, e) pairs: sum of exp(x - c) terms under a common max.
+__device__ __forceinline__ void merge_ce(float& c, float& e, float c2, float e2) {
+  const float nc = fmaxf(c, c2);
+  if (nc == neg_inf()) return;
+  const float a = (c == neg_inf()) ? 0.f : e * expf(c - nc);
+  const float b = (c2 == neg_inf()) ? 0.f : e2 * expf(c2 - nc);
+  c = nc;
+  e = a + b;
+}
+
+// Write one (h, t) row of the two block lists from 0/1 flags (generic
+// pointers: LDS or global).  Positions: a selected block goes to the number
+// of selected blocks before it; an unselected block goes after all selected
+// ones, at total_sel + (#unselected before it).
+__device__ void compact_row(const uint8_t* fsel, const uint8_t* fpr, int64_t Nb, int tot_sel,
+                            int tot_pr, int32_t* ids, int32_t* pids, int* red) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int run_s = 0, run_p = 0;
+  for (int64_t base = 0; base < Nb; base += kThreads) {
+    const int64_t b = base + tid;
+    const bool in = b < Nb;
+    const bool s = in && fsel[b];
+    const bool p = in && fpr[b];
+    const uint64_t ms = __ballot(s);
+    const uint64_t mp = __ballot(p);
+    if (lane == 0) {
+      red[w] = __popcll(ms);
+      red[4 + w] = __popcll(mp);
+    }
+    __syncthreads();
+    int off_s = 0, off_p = 0, sum_s = 0, sum_p = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int cs = red[i], cp = red[4 + i];
+      if (i < w) {
+        off_s += cs;
+        off_p += cp;
+      }
+      sum_s += cs;
+      sum_p += cp;
+    }
+    __syncthreads();
+    if (in) {
+      const int ps = run_s + off_s + __popcll(ms & below);  // selected before b
+      const int pp = run_p + off_p + __popcll(mp & below);
+      const int64_t pos_s = s ? ps : tot_sel + (b - ps);
+      const int64_t pos_p = p ? pp : tot_pr + (b - pp);
+      ids[pos_s] = static_cast<int32_t>(b);
+      pids[pos_p] = static_cast<int32_t>(b);
+    }
+    run_s += sum_s;
+    run_p += sum_p;
+  }
+}
+
+// Selection rule for block b of tile ti given its energy (selection.py:183-195).
+__device__ __forceinline__ bool select_rule(const SelectArgs& a, const TileInfo& ti, int64_t b,
+                                            bool energy_ok) {
+  const int64_t bs = b * a.bk;
+  const int64_t be = bs + a.bk;
+  const int64_t tail_from = a.Nt - a.last_n > 0 ? a.Nt - a.last_n : 0;
+  const bool forced = bs < a.sink || be > ti.tile_first - a.window || ti.t >= tail_from;
+  const bool visible = bs <= ti.tile_last;
+  return (energy_ok || forced) && visible;
+}
+
+// Shared tail: turn per-block (c_b, e_b) into the mask and lists.
+// cb/eb live in LDS and hold valid entries for b < ti.nfv.
+__device__ void finish_tile(const SelectArgs& a, const TileInfo& ti, float* cb, float* eb,
+                            uint8_t* fsel, uint8_t* fpr, float* fred, int* ired) {
+  const int tid = threadIdx.x;
+  float m = neg_inf();
+  for (int64_t b = tid; b < ti.nfv; b += kThreads) m = fmaxf(m, cb[b]);
+  m = block_max(m, fred);
+  float emax = 0.f;
+  for (int64_t b = tid; b < ti.nfv; b += kThreads) {
+    const float c = cb[b];
+    const float E = (c == neg_inf()) ? 0.f : eb[b] * expf(c - m);
+    eb[b] = E;
+    emax = fmaxf(emax, E);
+  }
+  emax = block_max(emax, fred);
+  const float thr = a.alpha * emax;
+  int ns = 0, np = 0;
+  for (int64_t b = tid; b < a.Nb; b += kThreads) {
+    const float E = (b < ti.nfv) ? eb[b] : 0.f;
+    const bool s = select_rule(a, ti, b, E >= thr);
+    const int64_t be = (b + 1) * a.bk;
+    const bool p = !s && (be < a.Lk ? be : a.Lk) <= ti.tile_first;
+    fsel[b] = s;
+    fpr[b] = p;
+    ns += s;
+    np += p;
+    if (a.sel_out) a.sel_out[(ti.h * a.Nt + ti.t) * a.Nb + b] = s;
+  }
+  if (!a.ids) return;
+  const int tot_s = block_sum_int(ns, ired);
+  const int tot_p = block_sum_int(np, ired);
+  __syncthreads();
+  const int64_t row = ti.h * a.Nt + ti.t;
+  compact_row(fsel, fpr, a.Nb, tot_s, tot_p, a.ids + row * a.Nb, a.pids + row * a.Nb, ired);
+  if (tid == 0) {
+    a.counts[row] = tot_s;
+    a.pcounts[row] = tot_p;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA path: bf16 / f16 queries and pooled keys, head_dim D (multiple of 16).
+// LDS: Q pass [128][D+8] (reused for the flag arrays), c_b[Nb], e_b[Nb].
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
+  constexpr int LDQ = D + 8;  // padded row: conflict-free 16-byte column reads
+  constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
+  float* cb = reinterpret_cast<float*>(smem + kRowsPerPass * LDQ * 2);
+  float* eb = cb + a.Nb;
+  __shared__ float fred[4];
+  __shared__ int ired[8];
+  __shared__ int rpos[kRowsPerPass];  // local query position, -1: no such row
+  __shared__ int rhead[kRowsPerPass]; // g of the packed row
+
+  const TileInfo ti = tile_info(a);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int hf = lane >> 5;
+  const int64_t R = a.G * a.tq;
+  const int64_t n_comp = a.scores ? a.Nb : ti.nfv;
+  const uint16_t* pk = static_cast<const uint16_t*>(a.pk) + ti.h * a.Nb * D;
+  const uint16_t* qbase = static_cast<const uint16_t*>(a.q);
+
+  for (int64_t b = tid; b < n_comp; b += kThreads) {
+    cb[b] = neg_inf();
+    eb[b] = 0.f;
+  }
+
+  for (int64_t rc = 0; rc < R; rc += kRowsPerPass) {
+    __syncthreads();
+    if (tid < kRowsPerPass) {
+      const int64_t pr = rc + tid;
+      int p = -1, gg = 0;
+      if (pr < R) {
+        gg = static_cast<int>(pr / a.tq);
+        p = static_cast<int>(ti.t * a.tq + (pr - gg * a.tq));
+      }
+      rpos[tid] = p;
+      rhead[tid] = gg;
+    }
+    // Stage 128 packed rows of Q (zeros past the tile or the valid length).
+    for (int e = tid; e < kRowsPerPass * (D / 8); e += kThreads) {
+      const int r = e / (D / 8);
+      const int c = e - r * (D / 8);
+      const int64_t pr = rc + r;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (pr < R) {
+        const int64_t g = pr / a.tq;
+        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
+        if (pos < a.Lq)
+          v = load16(qbase + (ti.h * a.G + g) * a.q_hs + pos * a.q_rs + c * 8);
+      }
+      store16(qs + r * LDQ + c * 8, v);
+    }
+    __syncthreads();
+    const int64_t rows_here = (R - rc) < kRowsPerPass ? (R - rc) : kRowsPerPass;
+    const int nrg = static_cast<int>((rows_here + 31) / 32);
+
+    for (int64_t chunk = wave; chunk * 32 < n_comp; chunk += 4) {
+      const int64_t b = chunk * 32 + l32;
+      // Rows see block b (fully visible blocks only) from local position lo.
+      const bool b_scored = b < ti.nfv;
+      int64_t lo64 = b * a.bk - a.offset;
+      const int lo = lo64 < 0 ? 0 : static_cast<int>(lo64 > 0x7fffffff ? 0x7fffffff : lo64);
+      const int lq = static_cast<int>(a.Lq);
+      typename Elem<T>::vec8 kf[KS];
+#pragma unroll
+      for (int k = 0; k < KS; ++k) {
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (b < a.Nb) v = load16(pk + b * D + k * 16 + hf * 8);
+        kf[k] = as_vec8<T>(v);
+      }
+      float cmax = neg_inf(), esum = 0.f;
+      for (int rg = 0; rg < nrg; ++rg) {
+        f32x16 acc = {};
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+          const u32x4 qv = load16(qs + (rg * 32 + l32) * LDQ + k * 16 + hf * 8);
+          acc = Elem<T>::mfma32(as_vec8<T>(qv), kf[k], acc);
+        }
+        // Lane holds rows rg*32 + (j/4)*8 + hf*4 + j%4 of block b.
+        float s[16];
+        bool ok[16];
+        float lm = neg_inf();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int r = rg * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
+          const int pos = rpos[r];
+          s[j] = acc[j] * a.scale;
+          if (a.scores && pos >= 0 && b < a.Nb)
+            a.scores[((ti.h * a.G + rhead[r]) * a.Lq_pad + pos) * a.Nb + b] = s[j];
+          const bool valid = b_scored && pos >= lo && pos < lq;
+          ok[j] = valid;
+          if (valid) lm = fmaxf(lm, s[j]);
+        }
+        if (lm != neg_inf()) {
+          const float nc = fmaxf(cmax, lm);
+          float e = (cmax == neg_inf()) ? 0.f : esum * expf(cmax - nc);
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (ok[j]) e += expf(s[j] - nc);
+          cmax = nc;
+          esum = e;
+        }
+      }
+      // Partner lane (hf ^ 1) holds the other 16 rows of each row group.
+      const float oc = __shfl_xor(cmax, 32);
+      const float oe = __shfl_xor(esum, 32);
+      merge_ce(cmax, esum, oc, oe);
+      if (hf == 0 && b < n_comp) {
+        float c = cb[b], e = eb[b];
+        merge_ce(c, e, cmax, esum);
+        cb[b] = c;
+        eb[b] = e;
+      }
+    }
+  }
+  __syncthreads();
+  // The Q staging area is free now: reuse it for the flag arrays.
+  uint8_t* fsel = reinterpret_cast<uint8_t*>(smem);
+  uint8_t* fpr = fsel + a.Nb;
+  finish_tile(a, ti, cb, eb, fsel, fpr, fred, ired);
+}
+
+// ---------------------------------------------------------------------------
+// Generic path (float32 inputs, or head dims without an MFMA instantiation).
+// LDS: Q pass [32][D] float, c_b[Nb], e_b[Nb], flags[2*Nb].
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float ld(const void* p, int64_t i);
+template <> __device__ __forceinline__ float ld<float>(const void* p, int64_t i) {
+  return static_cast<const float*>(p)[i];
+}
+template <> __device__ __forceinline__ float ld<bf16_t>(const void* p, int64_t i) {
+  return Elem<bf16_t>::to_float(static_cast<const uint16_t*>(p)[i]);
+}
+template <> __device__ __forceinline__ float ld<f16_t>(const void* p, int64_t i) {
+  return Elem<f16_t>::to_float(static_cast<const uint16_t*>(p)[i]);
+}
+
+constexpr int kGenericRows = 32;
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void select_generic_kernel(SelectArgs a, int D) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* qs = reinterpret_cast<float*>(smem);
+  float* cb = qs + kGenericRows * D;
+  float* eb = cb + a.Nb;
+  uint8_t* fsel = reinterpret_cast<uint8_t*>(eb + a.Nb);
+  uint8_t* fpr = fsel + a.Nb;
+  __shared__ float fred[4];
+  __shared__ int ired[8];
+  const TileInfo ti = tile_info(a);
+  const int tid = threadIdx.x;
+  const int64_t R = a.G * a.tq;
+  const int64_t n_comp = a.scores ? a.Nb : ti.nfv;
+  for (int64_t b = tid; b < n_comp; b += kThreads) {
+    cb[b] = neg_inf();
+    eb[b] = 0.f;
+  }
+  for (int64_t rc = 0; rc < R; rc += kGenericRows) {
+    __syncthreads();
+    for (int e = tid; e < kGenericRows * D; e += kThreads) {
+      const int r = e / D;
+      const int d = e - r * D;
+      const int64_t pr = rc + r;
+      float v = 0.f;
+      if (pr < R) {
+        const int64_t g = pr / a.tq;
+        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
+        if (pos < a.Lq) v = ld<T>(a.q, (ti.h * a.G + g) * a.q_hs + pos * a.q_rs + d);
+      }
+      qs[e] = v;
+    }
+    __syncthreads();
+    for (int64_t b = tid; b < n_comp; b += kThreads) {
+      float c = cb[b], e = eb[b];
+      for (int r = 0; r < kGenericRows && rc + r < R; ++r) {
+        const int64_t pr = rc + r;
+        float dot = 0.f;
+        for (int d = 0; d < D; ++d) dot = fmaf(qs[r * D + d], ld<T>(a.pk, (ti.h * a.Nb + b) * D + d), dot);
+        const float s = dot * a.scale;
+        const int64_t g = pr / a.tq;
+        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
+        if (a.scores) a.scores[((ti.h * a.G + g) * a.Lq_pad + pos) * a.Nb + b] = s;
+        if (pos < a.Lq && b < ti.nfv && b * a.bk <= a.offset + pos) merge_ce(c, e, s, 1.f);
+      }
+      cb[b] = c;
+      eb[b] = e;
+    }
+  }
+  __syncthreads();
+  finish_tile(a, ti, cb, eb, fsel, fpr, fred, ired);
+}
+
+// ---------------------------------------------------------------------------
+// Standalone compaction of a caller-provided mask (kernel.py:141-184).
+// ---------------------------------------------------------------------------
+struct CompactArgs {
+  const uint8_t* mask;
+  int64_t Hkv, Nt, Nb, tq, bk, offset, Lk;
+  int32_t *ids, *counts, *pids, *pcounts;
+};
+
+__global__ __launch_bounds__(kThreads) void compact_kernel(CompactArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint8_t* fsel = smem;
+  uint8_t* fpr = smem + a.Nb;
+  __shared__ int ired[8];
+  const int64_t row = blockIdx.x;
+  const int64_t t = row % a.Nt;
+  const int64_t tile_first = a.offset + t * a.tq;
+  const uint8_t* m = a.mask + row * a.Nb;
+  int ns = 0, np = 0;
+  for (int64_t b = threadIdx.x; b < a.Nb; b += kThreads) {
+    const bool s = m[b] != 0;
+    const int64_t be = (b + 1) * a.bk;
+    const bool p = !s && (be < a.Lk ? be : a.Lk) <= tile_first;
+    fsel[b] = s;
+    fpr[b] = p;
+    ns += s;
+    np += p;
+  }
+  const int tot_s = block_sum_int(ns, ired);
+  const int tot_p = block_sum_int(np, ired);
+  __syncthreads();
+  compact_row(fsel, fpr, a.Nb, tot_s, tot_p, a.ids + row * a.Nb, a.pids + row * a.Nb, ired);
+  if (threadIdx.x == 0) {
+    a.counts[row] = tot_s;
+    a.pcounts[row] = tot_p;
+  }
+}
+
+template <typename K>
+int launch_with_lds(K kernel, dim3 grid, size_t lds, hipStream_t stream, const SelectArgs& a) {
+  if (lds > 160 * 1024) return fail(FPV2_ERR_UNSUPPORTED, "score_select: %zu bytes of LDS exceed 160 KiB", lds);
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return fail(FPV2_ERR_LAUNCH, "score_select: hipFuncSetAttribute failed");
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, stream, a);
+  return check_launch("score_select");
+}
+
+template <typename K>
+int launch_generic(K kernel, dim3 grid, size_t lds, hipStream_t stream, const SelectArgs& a, int D) {
+  if (lds > 160 * 1024) return fail(FPV2_ERR_UNSUPPORTED, "score_select: %zu bytes of LDS exceed 160 KiB", lds);
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return fail(FPV2_ERR_LAUNCH, "score_select: hipFuncSetAttribute failed");
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), lds, stream, a, D);
+  return check_launch("score_select");
+}
+
+template <typename T>
+int dispatch_mfma(int64_t D, dim3 grid, hipStream_t stream, const SelectArgs& a, bool* done) {
+  *done = true;
+  const size_t tail = static_cast<size_t>(a.Nb) * 8;
+  switch (D) {
+    case 64: return launch_with_lds(select_mfma_kernel<T, 64>, grid, 128 * 72 * 2 + tail, stream, a);
+    case 96: return launch_with_lds(select_mfma_kernel<T, 96>, grid, 128 * 104 * 2 + tail, stream, a);
+    case 128: return launch_with_lds(select_mfma_kernel<T, 128>, grid, 128 * 136 * 2 + tail, stream, a);
+    case 256: return launch_with_lds(select_mfma_kernel<T, 256>, grid, 128 * 264 * 2 + tail, stream, a);
+    default: *done = false; return 0;
+  }
+}
+
+}  // namespace
+}  // namespace fpv2
+
+extern "C" int fpv2_score_select(const void* q, const void* pooled_k, int dtype,
+                                 const fpv2_select_params* p, uint8_t* selected, float* scores,
+                                 int32_t* selected_ids, int32_t* selected_counts,
+                                 int32_t* pruned_ids, int32_t* pruned_counts, void* stream) {
+  using namespace fpv2;
+  if (!p || !q || !pooled_k) return fail(FPV2_ERR_ARGUMENT, "score_select: null argument");
+  if (p->kv_heads <= 0 || p->query_heads <= 0 || p->query_heads % p->kv_heads)
+    return fail(FPV2_ERR_ARGUMENT, "query heads must be divisible by KV heads");
+  if (p->head_dim <= 0 || p->block_k <= 0 || p->tile_q <= 0 || p->num_blocks <= 0)
+    return fail(FPV2_ERR_ARGUMENT, "score_select: head_dim, block_k, tile_q and num_blocks must be positive");
+  if (p->padded_query_length <= 0 || p->padded_query_length % p->tile_q)
+    return fail(FPV2_ERR_ARGUMENT, "query length must be padded to a multiple of tile_q");
+  if (p->query_length <= 0 || p->query_length > p->padded_query_length)
+    return fail(FPV2_ERR_ARGUMENT, "query_length must be in (0, q.shape[-2]]");
+  if (p->offset < 0) return fail(FPV2_ERR_ARGUMENT, "offset must be non-negative");
+  if (p->offset + p->query_length > p->num_blocks * p->block_k)
+    return fail(FPV2_ERR_ARGUMENT, "queries extend beyond the represented key sequence");
+  if (p->num_blocks > FPV2_MAX_BLOCKS)
+    return fail(FPV2_ERR_UNSUPPORTED, "score_select: num_blocks %lld exceeds %d",
+                static_cast<long long>(p->num_blocks), FPV2_MAX_BLOCKS);
+  const bool any_list = selected_ids || selected_counts || pruned_ids || pruned_counts;
+  const bool all_list = selected_ids && selected_counts && pruned_ids && pruned_counts;
+  if (any_list && !all_list) return fail(FPV2_ERR_ARGUMENT, "score_select: give all four list outputs or none");
+  if (any_list && (p->key_length <= 0 || p->key_length > p->num_blocks * p->block_k))
+    return fail(FPV2_ERR_ARGUMENT, "key_length is inconsistent with selected blocks");
+  SelectArgs a{};
+  a.q = q;
+  a.pk = pooled_k;
+  a.Hkv = p->kv_heads;
+  a.G = p->query_heads / p->kv_heads;
+  a.Lq_pad = p->padded_query_length;
+  a.Nt = p->padded_query_length / p->tile_q;
+  a.Nb = p->num_blocks;
+  a.Lq = p->query_length;
+  a.Lk = p->key_length;
+  a.offset = p->offset;
+  a.bk = p->block_k;
+  a.tq = p->tile_q;
+  a.sink = p->sink_tokens;
+  a.window = p->window_tokens;
+  a.last_n = p->last_n_blocks;
+  a.scale = p->scale;
+  a.alpha = p->alpha;
+  a.q_hs = p->q_head_stride;
+  a.q_rs = p->q_row_stride;
+  a.sel_out = selected;
+  a.scores = scores;
+  a.ids = selected_ids;
+  a.counts = selected_counts;
+  a.pids = pruned_ids;
+  a.pcounts = pruned_counts;
+  const int64_t wgs = a.Hkv * a.Nt;
+  if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "score_select: grid too large");
+  dim3 grid(static_cast<unsigned>(wgs));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t D = p->head_dim;
+  const bool vec_ok = D % 8 == 0 && a.q_rs % 8 == 0 && a.q_hs % 8 == 0 &&
+                      reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(pooled_k) % 16 == 0;
+  bool done = false;
+  int rc = 0;
+  if (dtype == FPV2_BF16 && vec_ok) rc = dispatch_mfma<bf16_t>(D, grid, s, a, &done);
+  else if (dtype == FPV2_F16 && vec_ok) rc = dispatch_mfma<f16_t>(D, grid, s, a, &done);
+  if (done) return rc;
+  const size_t lds = static_cast<size_t>(kGenericRows) * D * 4 + static_cast<size_t>(a.Nb) * 10;
+  switch (dtype) {
+    case FPV2_F32: return launch_generic(select_generic_kernel<float>, grid, lds, s, a, static_cast<int>(D));
+    case FPV2_BF16: return launch_generic(select_generic_kernel<bf16_t>, grid, lds, s, a, static_cast<int>(D));
+    case FPV2_F16: return launch_generic(select_generic_kernel<f16_t>, grid, lds, s, a, static_cast<int>(D));
+    default: return fail(FPV2_ERR_UNSUPPORTED, "score_select: unsupported dtype %d", dtype);
+  }
+}
+
+extern "C" int fpv2_compact_block_indices(const uint8_t* selected, int64_t kv_heads,
+                                          int64_t num_tiles, int64_t num_blocks, int64_t tile_q,
+                                          int64_t block_k, int64_t offset, int64_t key_length,
+                                          int32_t* selected_ids, int32_t* selected_counts,
+                                          int32_t* pruned_ids, int32_t* pruned_counts,
+                                          void* stream) {
+  using namespace fpv2;
+  if (!selected || !selected_ids || !selected_counts || !pruned_ids || !pruned_counts)
+    return fail(FPV2_ERR_ARGUMENT, "compact: null argument");
+  if (kv_heads <= 0 || num_tiles <= 0 || num_blocks <= 0 || tile_q <= 0 || block_k <= 0)
+    return fail(FPV2_ERR_ARGUMENT, "compact: sizes must be positive");
+  if (offset < 0) return fail(FPV2_ERR_ARGUMENT, "offset must be non-negative");
+  if (key_length <= 0 || key_length > num_blocks * block_k)
+    return fail(FPV2_ERR_ARGUMENT, "key_length is inconsistent with selected blocks");
+  if (num_blocks * 2 > 160 * 1024) return fail(FPV2_ERR_UNSUPPORTED, "compact: too many blocks");
+  CompactArgs a{};
+  a.mask = selected;
+  a.Hkv = kv_heads;
+  a.Nt = num_tiles;
+  a.Nb = num_blocks;
+  a.tq = tile_q;
+  a.bk = block_k;
+  a.offset = offset;
+  a.Lk = key_length;
+  a.ids = selected_ids;
+  a.counts = selected_counts;
+  a.pids = pruned_ids;
+  a.pcounts = pruned_counts;
+  const int64_t rows = kv_heads * num_tiles;
+  if (rows > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "compact: grid too large");
+  const size_t lds = static_cast<size_t>(num_blocks) * 2;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(compact_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(lds)) != hipSuccess)
+    return fail(FPV2_ERR_LAUNCH, "compact: hipFuncSetAttribute failed");
+  hipLaunchKernelGGL(compact_kernel, dim3(static_cast<unsigned>(rows)), dim3(kThreads), lds,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("compact");
+}

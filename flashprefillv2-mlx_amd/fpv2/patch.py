@@ -1,0 +1,330 @@
+"""Model-independent, conservative hook for torch scaled-dot-product attention.
+
+Counterpart of the reference's ``fpv2/patch.py`` (which wraps MLX's
+``mx.fast.scaled_dot_product_attention``): ``enable`` replaces
+``torch.nn.functional.scaled_dot_product_attention`` with a wrapper that sends
+a call to FPV2 only when it is a batch-one, bottom-right causal prefill on a
+ROCm device with matching float16/bfloat16 Q/K/V, a supported head dimension,
+grouped-query-compatible head counts, at least one full query tile, and a key
+length meeting ``min_tokens``.  Everything else goes to the original function
+unchanged.
+
+Bottom-right causal in torch terms: ``is_causal=True`` with ``Lq == Lk`` (the
+top-left and bottom-right diagonals coincide), or ``attn_mask`` a
+``torch.nn.attention.bias.CausalBias`` of variant ``LOWER_RIGHT`` (or
+``UPPER_LEFT`` when square).  ``is_causal=True`` with ``Lq < Lk`` is top-left
+in torch and therefore passed through.
+
+For eligible calls ``offset = key_length - query_length`` places the query
+chunk in the causal key prefix.  Nothing is padded or copied: the kernels take
+head/row strides and valid lengths, treat rows past them as zeros, and write
+the ``[1, Hq, Lq, D]`` output directly.  ``disable`` restores the original.
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+from fpv2 import _lib
+from fpv2.kernel import SUPPORTED_HEAD_DIMS, _kernel_ready, _launch_attention
+from fpv2.selection import FPV2Config, _select_params
+
+try:  # torch >= 2.3
+    from torch.nn.attention.bias import CausalBias, CausalVariant
+except ImportError:  # pragma: no cover - older torch
+    CausalBias = CausalVariant = None
+
+_ORIGINAL_SDPA = F.scaled_dot_product_attention
+_enabled = False
+_collect_stats = False
+_selected_counts: list[torch.Tensor] = []
+_selected_dense_blocks = 0
+_visible_blocks = 0
+_PACKED_TILE_ROWS = 128
+
+
+def _effective_config(
+    config: FPV2Config, query_heads: int, kv_heads: int
+) -> FPV2Config | None:
+    """Resolve the default 128 packed rows into query positions (tile_q = 128 / G)."""
+    if config.tile_q != _PACKED_TILE_ROWS:
+        return config
+    if not kv_heads or query_heads % kv_heads:
+        return None
+    group_size = query_heads // kv_heads
+    if _PACKED_TILE_ROWS % group_size:
+        return None
+    return replace(config, tile_q=_PACKED_TILE_ROWS // group_size)
+
+
+def _request_config(
+    config: FPV2Config, key_length: int, total_tokens: int | None
+) -> FPV2Config:
+    """Apply the dense tail only when this call reaches the request boundary."""
+    if config.last_n_blocks and (total_tokens is None or key_length < total_tokens):
+        return replace(config, last_n_blocks=0)
+    return config
+
+
+def _causal_block_count(kv_heads: int, query_length: int, offset: int,
+                        config: FPV2Config) -> int:
+    count = 0
+    for start in range(0, query_length, config.tile_q):
+        end = offset + min(start + config.tile_q, query_length)
+        count += (end + config.block_k - 1) // config.block_k
+    return count * kv_heads
+
+
+def block_sparsity() -> float:
+    """Fraction of visible causal blocks skipped since ``enable``.
+
+    Selected counts stay on the device until this call, which synchronises
+    once to read their sum.
+    """
+    if not _visible_blocks:
+        return 0.0
+    selected = _selected_dense_blocks
+    if _selected_counts:
+        total = torch.stack([c.sum(dtype=torch.int64) for c in _selected_counts]).sum()
+        selected += int(total.item())
+    return 1.0 - selected / _visible_blocks
+
+
+def _pad_sequence(x: torch.Tensor, length: int) -> torch.Tensor:
+    """Zero-pad the sequence (penultimate) axis to ``length``."""
+    amount = length - x.shape[-2]
+    if amount < 0:
+        raise ValueError("target length cannot be shorter than the input")
+    if not amount:
+        return x
+    return F.pad(x, (0, 0, 0, amount))
+
+
+def fpv2_sdpa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    scale: float,
+    config: FPV2Config = FPV2Config(),
+) -> torch.Tensor:
+    """Apply FPV2 to a batch-one, bottom-right causal attention ``[1, H, L, D]``.
+
+    Data flow of the reference (``fpv2/patch.py:102-174``) without the
+    padding copies: pool K/V (one launch), score/select/compact (one launch),
+    sparse attention (one launch), all on the current stream, no host sync.
+    """
+    return _fpv2_sdpa(q, k, v, scale=scale, config=config)
+
+
+def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
+    """``fpv2_sdpa`` body.  ``marks(name)`` (optional) is called on the host
+    between the launches ("select", "attention", "done") so a caller can
+    record stream events around each kernel; ``keep`` (optional dict)
+    receives the pooled tensors and block lists of the call."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have shape [batch, heads, sequence, dim]")
+    if q.shape[0] != 1 or k.shape[0] != 1 or v.shape[0] != 1:
+        raise ValueError("FPV2 currently supports batch size 1")
+    effective_config = _effective_config(config, q.shape[1], k.shape[1])
+    if effective_config is None:
+        raise ValueError("GQA group size must divide 128 packed query rows")
+    config = effective_config
+    query_length = q.shape[-2]
+    key_length = k.shape[-2]
+    if query_length > key_length:
+        raise ValueError("query length cannot exceed key length for causal attention")
+    if k.shape != v.shape or q.shape[-1] != k.shape[-1]:
+        raise ValueError("q, k, and v head dimensions must match")
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head dimension must be one of {SUPPORTED_HEAD_DIMS}")
+    if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, and v must share float16 or bfloat16 dtype")
+    offset = key_length - query_length
+
+    query_heads, kv_heads, head_dim = q.shape[1], k.shape[1], q.shape[-1]
+    padded_query_length = -(-query_length // config.tile_q) * config.tile_q
+    required_key_length = max(key_length, offset + padded_query_length)
+    padded_key_length = -(-required_key_length // config.block_k) * config.block_k
+    num_tiles = padded_query_length // config.tile_q
+    num_blocks = padded_key_length // config.block_k
+    if num_blocks > _lib.MAX_BLOCKS:
+        raise ValueError(f"key length needs {num_blocks} blocks; at most {_lib.MAX_BLOCKS}")
+
+    device = _lib.require_device(q, k, v)
+    lib = _lib.load()
+    q3, k3, v3 = _kernel_ready(q[0]), _kernel_ready(k[0]), _kernel_ready(v[0])
+    stream = _lib.stream_ptr(device)
+    dtype = _lib.dtype_code(q.dtype)
+
+    pooled_k = torch.empty((kv_heads, num_blocks, head_dim), dtype=q.dtype, device=device)
+    pooled_v = torch.empty_like(pooled_k)
+    ids = torch.empty((kv_heads, num_tiles, num_blocks), dtype=torch.int32, device=device)
+    pruned_ids = torch.empty_like(ids)
+    counts = torch.empty((kv_heads, num_tiles), dtype=torch.int32, device=device)
+    pruned_counts = torch.empty_like(counts)
+    with torch.cuda.device(device):
+        if marks is not None:
+            marks("pool")
+        if k3.stride() == v3.stride():
+            status = lib.fpv2_pool_kv(
+                k3.data_ptr(), v3.data_ptr(), pooled_k.data_ptr(), pooled_v.data_ptr(),
+                dtype, kv_heads, key_length, num_blocks, head_dim, config.block_k,
+                k3.stride(0), k3.stride(1), stream)
+            _lib.check(status, "pool_kv")
+        else:
+            for src, dst in ((k3, pooled_k), (v3, pooled_v)):
+                status = lib.fpv2_pool_blocks(
+                    src.data_ptr(), dst.data_ptr(), dtype, kv_heads, key_length,
+                    num_blocks, head_dim, config.block_k, src.stride(0), src.stride(1),
+                    stream)
+                _lib.check(status, "pool_blocks")
+        params = _select_params(q3, num_blocks, kv_heads=kv_heads, scale=scale,
+                                config=config, offset=offset, query_length=query_length,
+                                padded_length=padded_query_length, key_length=key_length)
+        if marks is not None:
+            marks("select")
+        status = lib.fpv2_score_select(
+            q3.data_ptr(), pooled_k.data_ptr(), dtype, params, None, None, ids.data_ptr(),
+            counts.data_ptr(), pruned_ids.data_ptr(), pruned_counts.data_ptr(), stream)
+        _lib.check(status, "score_select")
+    if _collect_stats:
+        global _visible_blocks
+        _selected_counts.append(counts)
+        _visible_blocks += _causal_block_count(kv_heads, query_length, offset, config)
+    out = torch.empty((1, query_heads, query_length, head_dim), dtype=q.dtype, device=device)
+    if marks is not None:
+        marks("attention")
+    _launch_attention(
+        q3, k3, v3, pooled_k, pooled_v, ids, counts, pruned_ids, pruned_counts, out[0],
+        device=device, scale=scale, config=config, offset=offset,
+        query_length=query_length, key_length=key_length, num_blocks=num_blocks,
+        padded_query_length=padded_query_length, out_rows=query_length)
+    if marks is not None:
+        marks("done")
+    if keep is not None:
+        keep.update(config=config, offset=offset, pooled_k=pooled_k, pooled_v=pooled_v,
+                    lists=(ids, counts, pruned_ids, pruned_counts))
+    return out
+
+
+def _bottom_right_causal(q, k, attn_mask, is_causal) -> bool:
+    query_length, key_length = q.shape[-2], k.shape[-2]
+    if attn_mask is None:
+        return bool(is_causal) and query_length == key_length
+    if is_causal or CausalBias is None or not isinstance(attn_mask, CausalBias):
+        return False
+    if attn_mask.seq_len_q != query_length or attn_mask.seq_len_kv != key_length:
+        return False
+    if attn_mask.variant == CausalVariant.LOWER_RIGHT:
+        return True
+    return attn_mask.variant == CausalVariant.UPPER_LEFT and query_length == key_length
+
+
+def _eligible(q, k, v, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
+              config: FPV2Config, min_tokens: int) -> bool:
+    if kwargs or dropout_p:
+        return False
+    if not all(isinstance(t, torch.Tensor) for t in (q, k, v)):
+        return False
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        return False
+    if q.shape[0] != 1 or k.shape[0] != 1 or v.shape[0] != 1:
+        return False
+    if k.shape != v.shape or q.shape[-1] != k.shape[-1]:
+        return False
+    if q.shape[-2] > k.shape[-2] or q.shape[-2] < config.tile_q:
+        return False
+    if k.shape[-2] < min_tokens:
+        return False
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        return False
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        return False
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        return False
+    if not (q.device.type == "cuda" and k.device == q.device and v.device == q.device):
+        return False
+    if q.requires_grad or k.requires_grad or v.requires_grad:
+        return False  # forward-only kernel
+    if not k.shape[1] or q.shape[1] % k.shape[1]:
+        return False
+    if q.shape[1] != k.shape[1] and not enable_gqa:
+        return False
+    return _bottom_right_causal(q, k, attn_mask, is_causal)
+
+
+def enable(
+    config: FPV2Config | None = None,
+    *,
+    min_tokens: int = 4_096,
+    collect_stats: bool = False,
+    total_tokens: int | None = None,
+    **config_fields: Any,
+) -> None:
+    """Replace torch SDPA with an FPV2-gated, request-aware wrapper."""
+    global _collect_stats, _enabled, _selected_dense_blocks, _visible_blocks
+    if min_tokens <= 0:
+        raise ValueError("min_tokens must be positive")
+    if not isinstance(collect_stats, bool):
+        raise ValueError("collect_stats must be a boolean")
+    if total_tokens is not None and (
+        not isinstance(total_tokens, int)
+        or isinstance(total_tokens, bool)
+        or total_tokens <= 0
+    ):
+        raise ValueError("total_tokens must be a positive integer or None")
+    if config is not None and config_fields:
+        config = replace(config, **config_fields)
+    elif config is None:
+        config = FPV2Config(**config_fields)
+    _collect_stats = collect_stats
+    _selected_counts.clear()
+    _selected_dense_blocks = 0
+    _visible_blocks = 0
+
+    def wrapped(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
+                scale=None, enable_gqa=False, **kwargs):
+        four_d = all(isinstance(t, torch.Tensor) and t.ndim == 4 for t in (query, key))
+        call_config = _effective_config(config, query.shape[1], key.shape[1]) if four_d else None
+        if call_config is not None:
+            call_config = _request_config(call_config, key.shape[-2], total_tokens)
+        if call_config is not None and _eligible(
+            query, key, value, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
+            call_config, min_tokens
+        ):
+            call_scale = query.shape[-1] ** -0.5 if scale is None else scale
+            return fpv2_sdpa(query, key, value, scale=call_scale, config=call_config)
+        if _collect_stats and call_config is not None and _eligible(
+            query, key, value, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
+            call_config, 1
+        ):
+            global _selected_dense_blocks, _visible_blocks
+            visible = _causal_block_count(
+                key.shape[1], query.shape[-2], key.shape[-2] - query.shape[-2], call_config
+            )
+            _selected_dense_blocks += visible
+            _visible_blocks += visible
+        return _ORIGINAL_SDPA(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                              is_causal=is_causal, scale=scale, enable_gqa=enable_gqa,
+                              **kwargs)
+
+    F.scaled_dot_product_attention = wrapped
+    _enabled = True
+
+
+def disable() -> None:
+    """Restore torch's original scaled dot-product attention."""
+    global _collect_stats, _enabled
+    F.scaled_dot_product_attention = _ORIGINAL_SDPA
+    _collect_stats = False
+    _enabled = False
+
+
+def is_enabled() -> bool:
+    """Whether the FPV2 SDPA hook is installed."""
+    return _enabled

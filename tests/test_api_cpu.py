@@ -1,0 +1,251 @@
+"""Host-side behaviour of the product package (no GPU needed).
+
+Validation messages follow the reference's tests (``tests/test_selection.py``,
+``tests/test_kernel.py``, ``tests/test_patch.py``); the hook must pass every
+ineligible call (here: CPU tensors, array masks, decode shapes) to torch's
+original SDPA unchanged; the C-ABI library must load and export every symbol
+``include/fpv2.h`` declares; and compute entry points must refuse non-GPU
+tensors instead of falling back.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import fpv2
+from fpv2 import FPV2Config, block_sparsity, disable, enable, pool_blocks
+from fpv2 import _lib
+from fpv2.kernel import (TileConfig, compact_block_indices, default_tile, sparse_attention,
+                         _tile_for_config)
+from fpv2.patch import _ORIGINAL_SDPA, _effective_config, _request_config
+from fpv2.selection import block_scores_and_select, density
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+@pytest.fixture(autouse=True)
+def restore_sdpa():
+    disable()
+    yield
+    disable()
+
+
+# ---- FPV2Config (selection.py:30-65) -------------------------------------
+
+@pytest.mark.parametrize("value", [0, -1, 1.5, True])
+def test_score_chunk_tiles_must_be_a_positive_integer(value):
+    with pytest.raises(ValueError, match="score_chunk_tiles"):
+        FPV2Config(score_chunk_tiles=value)
+
+
+def test_pack_gqa_must_be_boolean():
+    with pytest.raises(ValueError, match="pack_gqa"):
+        FPV2Config(pack_gqa=1)
+
+
+@pytest.mark.parametrize("value", [-1, 1.5, True])
+def test_last_n_blocks_must_be_a_non_negative_integer(value):
+    with pytest.raises(ValueError, match="last_n_blocks"):
+        FPV2Config(last_n_blocks=value)
+
+
+def test_config_defaults_and_other_rules():
+    c = FPV2Config()
+    assert (c.block_k, c.tile_q, c.alpha, c.sink_tokens, c.window_tokens, c.last_n_blocks,
+            c.mean_correction, c.score_chunk_tiles, c.pack_gqa) == (
+        128, 128, 0.1, 256, 384, 2, True, None, False)
+    with pytest.raises(ValueError, match="positive"):
+        FPV2Config(block_k=0)
+    with pytest.raises(ValueError, match="alpha"):
+        FPV2Config(alpha=-0.1)
+    with pytest.raises(ValueError, match="non-negative"):
+        FPV2Config(window_tokens=-1)
+
+
+# ---- validation before any device work ----------------------------------
+
+def test_pool_blocks_rejects_unaligned_length():
+    with pytest.raises(ValueError, match="divisible"):
+        pool_blocks(torch.zeros((2, 7, 4)), 4)
+
+
+def test_compaction_rejects_non_boolean_mask():
+    with pytest.raises(ValueError, match="boolean"):
+        compact_block_indices(torch.ones((1, 1, 1), dtype=torch.int32))
+
+
+def test_selection_input_validation():
+    cfg = FPV2Config(block_k=16, tile_q=16)
+    with pytest.raises(ValueError, match="divisible by KV heads"):
+        block_scores_and_select(torch.zeros(3, 16, 8), torch.zeros(2, 1, 8), scale=1.0, config=cfg)
+    with pytest.raises(ValueError, match="padded to a multiple of tile_q"):
+        block_scores_and_select(torch.zeros(2, 15, 8), torch.zeros(2, 1, 8), scale=1.0, config=cfg)
+    with pytest.raises(ValueError, match="beyond the represented key sequence"):
+        block_scores_and_select(torch.zeros(2, 32, 8), torch.zeros(2, 1, 8), scale=1.0, config=cfg)
+
+
+def test_sparse_attention_validation():
+    cfg = FPV2Config(block_k=16, tile_q=16)
+    q = torch.zeros(4, 32, 64, dtype=torch.bfloat16)
+    k = torch.zeros(2, 32, 64, dtype=torch.bfloat16)
+    ids = torch.zeros(2, 2, 2, dtype=torch.int32)
+    cnt = torch.zeros(2, 2, dtype=torch.int32)
+    pk = torch.zeros(2, 2, 64)
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        sparse_attention(q.float(), k.float(), k.float(), pk, pk, ids, cnt, ids, cnt,
+                         scale=1.0, config=cfg)
+    with pytest.raises(ValueError, match="head dimension"):
+        sparse_attention(q[..., :48], k[..., :48], k[..., :48], pk, pk, ids, cnt, ids, cnt,
+                         scale=1.0, config=cfg)
+    with pytest.raises(ValueError, match="int32"):
+        sparse_attention(q, k, k, pk, pk, ids.long(), cnt, ids, cnt, scale=1.0, config=cfg)
+    with pytest.raises(ValueError, match="block lists must have shape"):
+        sparse_attention(q, k, k, pk, pk, ids[:, :1], cnt, ids, cnt, scale=1.0, config=cfg)
+    q6 = torch.zeros(6, 32, 64, dtype=torch.bfloat16)  # G = 3 does not divide bq = 16
+    with pytest.raises(ValueError, match="PackGQA"):
+        sparse_attention(q6, k, k, pk, pk, ids, cnt, ids, cnt, scale=1.0, config=cfg,
+                         pack_gqa=True)
+
+
+def test_compute_entry_points_refuse_cpu_tensors():
+    with pytest.raises(RuntimeError, match="ROCm"):
+        pool_blocks(torch.zeros(2, 8, 4), 4)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        compact_block_indices(torch.zeros(1, 1, 2, dtype=torch.bool),
+                              config=FPV2Config(block_k=16, tile_q=16))
+
+
+def test_density_on_host_mask():
+    cfg = FPV2Config(block_k=4, tile_q=4)
+    sel = torch.zeros(2, 4, 4, dtype=torch.bool)
+    sel[:, torch.arange(4), torch.arange(4)] = True
+    assert density(sel, config=cfg).item() == pytest.approx(0.4)
+
+
+# ---- tiles (kernel.py:30-88) ----------------------------------------------
+
+def test_default_tile_dispatch():
+    assert default_tile(64) == TileConfig(32, 32, 4)
+    assert default_tile(96) == TileConfig(32, 32, 4)
+    assert default_tile(128) == TileConfig(64, 32, 8)
+    assert default_tile(256) == TileConfig(32, 16, 4)
+    with pytest.raises(ValueError, match="head dimension"):
+        default_tile(80)
+
+
+def test_tile_fallback_for_hook_tile():
+    # The hook's 32-position tile falls back to (32, 16, 4) (kernel.py:76-88).
+    assert _tile_for_config(128, FPV2Config(tile_q=32)) == TileConfig(32, 16, 4)
+    with pytest.raises(ValueError, match="32 KB"):
+        TileConfig(64, 64, 8).check(256, block_k=128, tile_q=128)
+
+
+# ---- hook helpers (patch.py:41-63) -----------------------------------------
+
+def test_default_tile_uses_128_packed_gqa_rows():
+    effective = _effective_config(FPV2Config(), query_heads=32, kv_heads=8)
+    assert effective is not None and effective.tile_q == 32
+    custom = FPV2Config(tile_q=64)
+    assert _effective_config(custom, query_heads=32, kv_heads=8) is custom
+
+
+def test_dense_tail_is_applied_only_at_known_request_end():
+    config = FPV2Config(last_n_blocks=2)
+    assert _request_config(config, 2_048, 8_192).last_n_blocks == 0
+    assert _request_config(config, 8_192, 8_192) is config
+    assert _request_config(config, 8_192, None).last_n_blocks == 0
+
+
+@pytest.mark.parametrize("value", [0, -1, 1.5, True])
+def test_total_tokens_must_be_a_positive_integer(value):
+    with pytest.raises(ValueError, match="total_tokens"):
+        enable(total_tokens=value)
+
+
+def test_enable_disable_swap_torch_sdpa():
+    assert F.scaled_dot_product_attention is _ORIGINAL_SDPA
+    enable(min_tokens=1)
+    assert fpv2.is_enabled() and F.scaled_dot_product_attention is not _ORIGINAL_SDPA
+    disable()
+    assert not fpv2.is_enabled() and F.scaled_dot_product_attention is _ORIGINAL_SDPA
+
+
+def _inputs(length, query_length=None, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(7)
+    query_length = length if query_length is None else query_length
+    q = torch.randn((1, 4, query_length, 64), generator=g).to(dtype)
+    k = torch.randn((1, 2, length, 64), generator=g).to(dtype)
+    v = torch.randn((1, 2, length, 64), generator=g).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize(("length", "query_length", "causal"),
+                         [(64, 64, True), (128, 1, True), (128, 32, True), (128, 128, False),
+                          (256, 256, True)])
+def test_ineligible_cpu_calls_are_bit_identical(length, query_length, causal):
+    q, k, v = _inputs(length, query_length)
+    expected = _ORIGINAL_SDPA(q, k, v, is_causal=causal, enable_gqa=True)
+    enable(min_tokens=128, collect_stats=True)
+    actual = F.scaled_dot_product_attention(q, k, v, is_causal=causal, enable_gqa=True)
+    assert torch.equal(actual, expected)
+
+
+def test_array_mask_falls_through_and_disable_restores_original():
+    q, k, v = _inputs(128)
+    mask = torch.zeros((128, 128), dtype=torch.bfloat16)
+    expected = _ORIGINAL_SDPA(q, k, v, attn_mask=mask, enable_gqa=True)
+    enable(min_tokens=1)
+    actual = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
+    assert torch.equal(actual, expected)
+    disable()
+    assert F.scaled_dot_product_attention is _ORIGINAL_SDPA
+
+
+def test_block_sparsity_starts_at_zero():
+    enable(min_tokens=1, collect_stats=True)
+    assert block_sparsity() == 0.0
+
+
+# ---- C ABI -----------------------------------------------------------------
+
+def _declared_symbols() -> set[str]:
+    text = (ROOT / "include" / "fpv2.h").read_text()
+    return set(re.findall(r"^\s*(?:int|const char\*)\s+(fpv2_\w+)\s*\(", text, re.M))
+
+
+def test_header_declares_the_bound_symbols():
+    assert _declared_symbols() == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libfpv2_hip.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    loaded = _lib.load()
+    assert loaded.fpv2_abi_version() == _lib.ABI_VERSION
+
+
+def test_abi_struct_layouts_match_header():
+    # every int64 field is 8-byte aligned; the float pair / int32+double padding
+    assert ctypes.sizeof(_lib.SelectParams) == 8 * 15 + 8
+    assert ctypes.sizeof(_lib.AttnParams) == 8 * 11 + 8 + 8 + 8 * 8
+
+
+def test_library_rejects_bad_arguments_without_a_gpu():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libfpv2_hip.so not built")
+    lib = _lib.load()
+    status = lib.fpv2_pool_blocks(None, None, _lib.BF16, 1, 8, 1, 8, 8, 64, 8, None)
+    assert status == _lib.FPV2_ERR_ARGUMENT
+    assert b"null" in lib.fpv2_last_error()
+    params = _lib.AttnParams(query_heads=3, kv_heads=2)
+    status = lib.fpv2_sparse_attention(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, _lib.BF16, params, None)
+    assert status == _lib.FPV2_ERR_ARGUMENT

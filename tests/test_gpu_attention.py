@@ -1,0 +1,151 @@
+"""GPU parity: block-sparse attention with mean correction vs the oracle.
+
+Two comparisons per case:
+  * same selection, same pooled values: the device output against the
+    oracle's blockwise float32 evaluation of exactly the blocks the device
+    visited — max-abs <= 2e-2 and mean-abs <= 2e-3 (the bf16 bar);
+  * the reference's own check (``tests/test_kernel.py:18-63,89-132``):
+    relative max error < 2e-2 against the literal float32
+    ``fpv2_attention_reference`` restatement, which selects on float32
+    pooled keys.
+Parameter grids follow the reference's kernel tests.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import attention_errors, to_np
+from oracle import fpv2_oracle as orc
+from fpv2 import FPV2Config, pool_blocks
+from fpv2.kernel import TileConfig, compact_block_indices, sparse_attention
+from fpv2.selection import block_scores_and_select
+from fpv2.synthetic import structured_qkv
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS, REL = 2e-2, 2e-3, 2e-2
+
+
+def _cfg(c: FPV2Config) -> orc.OracleConfig:
+    return orc.OracleConfig(**{f: getattr(c, f) for f in orc.OracleConfig.__dataclass_fields__})
+
+
+def _run_and_check(cuda, q, k, v, config, *, offset=0, pack_gqa=False, tile=None,
+                   dtype=torch.bfloat16):
+    scale = q.shape[-1] ** -0.5
+    qd, kd, vd = (x.to(dtype).to(cuda) for x in (q, k, v))
+    pk = pool_blocks(kd, config.block_k)
+    pv = pool_blocks(vd, config.block_k)
+    selected, _ = block_scores_and_select(qd, pk, scale=scale, config=config, offset=offset)
+    lists = compact_block_indices(selected, config=config, offset=offset,
+                                  query_length=q.shape[1], key_length=k.shape[1])
+    out = sparse_attention(qd, kd, vd, pk, pv, *lists, scale=scale, config=config,
+                           offset=offset, pack_gqa=pack_gqa, tile=tile)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and out.shape == q.shape
+    got = to_np(out)
+    qn, kn, vn = (to_np(x.to(dtype)) for x in (q, k, v))
+    # (1) same selection and pooled values as the device
+    same = orc.fpv2_attention_blockwise(qn, kn, vn, scale=scale, selected=to_np(selected),
+                                        pooled_k=to_np(pk), pooled_v=to_np(pv), config=_cfg(config),
+                                        offset=offset)
+    err = attention_errors(got, same)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+    # (2) the reference's comparison against the float32 dense reference
+    ref = orc.fpv2_attention_reference(qn, kn, vn, scale=scale, config=_cfg(config),
+                                       offset=offset)
+    assert attention_errors(got, ref)["rel"] < REL
+    return got, selected
+
+
+@pytest.mark.parametrize("mean_correction", [False, True])
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+@pytest.mark.parametrize("pack_gqa", [False, True])
+def test_kernel_matches_reference(cuda, mean_correction, head_dim, pack_gqa):
+    # tests/test_kernel.py:18-63
+    config = FPV2Config(block_k=16, tile_q=16, alpha=0.15, sink_tokens=16, window_tokens=16,
+                        mean_correction=mean_correction)
+    q, k, v = structured_qkv(length=64, query_heads=4, kv_heads=2, head_dim=head_dim,
+                             block_size=16)
+    _run_and_check(cuda, q, k, v, config, pack_gqa=pack_gqa)
+
+
+@pytest.mark.parametrize("pack_gqa", [False, True])
+@pytest.mark.parametrize(("alpha", "mean_correction"), [(0.0, False), (0.15, False), (0.15, True)])
+def test_real_block_kernel_modes(cuda, alpha, mean_correction, pack_gqa):
+    # tests/test_kernel.py:135-155
+    config = FPV2Config(alpha=alpha, sink_tokens=128, window_tokens=256,
+                        mean_correction=mean_correction)
+    q, k, v = structured_qkv(length=2048, query_heads=8, kv_heads=2, head_dim=128, seed=31)
+    _run_and_check(cuda, q, k, v, config, pack_gqa=pack_gqa)
+
+
+@pytest.mark.parametrize(("offset", "query_length"), [(1024, 1024), (1920, 128)])
+def test_chunk_offset_kernel(cuda, offset, query_length):
+    # tests/test_kernel.py:158-178
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256, mean_correction=True)
+    full_q, k, v = structured_qkv(length=2048, query_heads=8, kv_heads=2, head_dim=128, seed=37)
+    q = full_q[:, offset:offset + query_length]
+    _run_and_check(cuda, q, k, v, config, offset=offset)
+
+
+@pytest.mark.parametrize("head_dim", [64, 96, 256])
+def test_real_block_supported_head_dims(cuda, head_dim):
+    # tests/test_kernel.py:181-197
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256, mean_correction=True)
+    q, k, v = structured_qkv(length=2048, query_heads=8, kv_heads=2, head_dim=head_dim, seed=41)
+    _run_and_check(cuda, q, k, v, config)
+
+
+def test_multi_fragment_rows_match_reference(cuda):
+    # tests/test_kernel.py:207-219
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256)
+    q, k, v = structured_qkv(length=2048, query_heads=8, kv_heads=2, head_dim=128, seed=43)
+    _run_and_check(cuda, q, k, v, config, tile=TileConfig(64, 32, 4))
+
+
+def test_float16_path(cuda):
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256)
+    q, k, v = structured_qkv(length=1024, query_heads=8, kv_heads=2, head_dim=128, seed=47)
+    _run_and_check(cuda, q, k, v, config, dtype=torch.float16)
+
+
+def test_alpha_zero_equals_exact_causal_attention(cuda):
+    config = FPV2Config(block_k=64, tile_q=64, alpha=0, sink_tokens=0, window_tokens=0,
+                        mean_correction=False)
+    q, k, v = structured_qkv(length=640, query_heads=8, kv_heads=2, head_dim=128, seed=3)
+    got, selected = _run_and_check(cuda, q, k, v, config)
+    exact = orc.exact_causal_attention(*(to_np(x.bfloat16()) for x in (q, k, v)), 128 ** -0.5)
+    err = attention_errors(got, exact)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+def test_correction_phase_with_many_pruned_blocks(cuda):
+    # high-contrast clusters prune most blocks: the pooled phase spans > 64 entries
+    config = FPV2Config(block_k=16, tile_q=16, alpha=0.5, sink_tokens=16, window_tokens=16,
+                        mean_correction=True)
+    q, k, v = structured_qkv(length=2048, query_heads=4, kv_heads=2, head_dim=128,
+                             block_size=16, noise=0.05, seed=53)
+    _, selected = _run_and_check(cuda, q, k, v, config)
+    pruned = (~selected.cpu()).sum(-1)
+    assert int(pruned.max()) > 64
+
+
+def test_out_of_range_lists_are_clipped(cuda):
+    # ids outside [0, Nb) and counts outside [0, Nb] are clipped (kernel.py:555-558)
+    config = FPV2Config(block_k=32, tile_q=32, alpha=0, sink_tokens=0, window_tokens=0,
+                        mean_correction=True)
+    q, k, v = structured_qkv(length=128, query_heads=2, kv_heads=1, head_dim=64, block_size=32,
+                             dtype=torch.bfloat16, device=cuda)
+    pk, pv = pool_blocks(k, 32), pool_blocks(v, 32)
+    nb = 4
+    ids = torch.full((1, 4, nb), 99, dtype=torch.int32, device=cuda)
+    cnt = torch.full((1, 4), 1000, dtype=torch.int32, device=cuda)
+    pids = torch.full((1, 4, nb), -5, dtype=torch.int32, device=cuda)
+    pcnt = torch.full((1, 4), -3, dtype=torch.int32, device=cuda)
+    out = sparse_attention(q, k, v, pk, pv, ids, cnt, pids, pcnt, scale=0.125, config=config)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()

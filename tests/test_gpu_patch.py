@@ -1,0 +1,185 @@
+"""GPU parity of the SDPA hook (``fpv2/patch.py`` counterpart).
+
+Reference tests restated (``tests/test_patch.py``): alpha=0 equals stock
+attention for padded, unaligned-chunk and real shapes; ineligible calls are
+bit-identical; tile-aligned chunks equal single-shot FPV2; sparsity accounting.
+"Stock attention" is computed on the CPU in float32 (a textbook softmax),
+never with bf16 batched products on the GPU.  BASELINE config 1 (8k, Qwen3-4B
+geometry) and its high-contrast variant are checked end to end against the
+oracle's hook data flow on a subset of query tiles.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import attention_errors, to_np
+from oracle import fpv2_oracle as orc
+from fpv2 import FPV2Config, block_sparsity, disable, enable, fpv2_sdpa
+from fpv2.patch import _ORIGINAL_SDPA, _request_config
+from fpv2.synthetic import baseline_qkv, structured_qkv
+
+pytestmark = pytest.mark.gpu
+
+try:
+    from torch.nn.attention.bias import causal_lower_right
+except ImportError:  # pragma: no cover
+    causal_lower_right = None
+
+MAX_ABS, MEAN_ABS, REL = 2e-2, 2e-3, 2e-2
+
+
+@pytest.fixture(autouse=True)
+def restore_sdpa():
+    disable()
+    yield
+    disable()
+
+
+def _inputs(length, query_length=None, *, heads=(4, 2), dim=64, seed=7):
+    g = torch.Generator().manual_seed(seed)
+    query_length = length if query_length is None else query_length
+    q = torch.randn((1, heads[0], query_length, dim), generator=g).bfloat16()
+    k = torch.randn((1, heads[1], length, dim), generator=g).bfloat16()
+    v = torch.randn((1, heads[1], length, dim), generator=g).bfloat16()
+    return q, k, v
+
+
+def _stock(q, k, v, scale):
+    """Bottom-right causal softmax attention on the CPU in float32."""
+    q, k, v = (x.float().cpu() for x in (q, k, v))
+    g = q.shape[1] // k.shape[1]
+    k, v = k.repeat_interleave(g, 1), v.repeat_interleave(g, 1)
+    lq, lk = q.shape[-2], k.shape[-2]
+    mask = torch.arange(lk)[None, :] <= (lk - lq + torch.arange(lq))[:, None]
+    return _ORIGINAL_SDPA(q, k, v, attn_mask=mask, scale=scale).numpy()
+
+
+def _hook_call(q, k, v, scale):
+    lq, lk = q.shape[-2], k.shape[-2]
+    if lq == lk:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale,
+                                              enable_gqa=True)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=causal_lower_right(lq, lk),
+                                          scale=scale, enable_gqa=True)
+
+
+@pytest.mark.parametrize(("length", "query_length"), [(130, 130), (190, 128)])
+def test_alpha_zero_padded_and_unaligned_calls_match_stock(cuda, length, query_length):
+    # tests/test_patch.py:44-73
+    q, k, v = _inputs(length, query_length)
+    expected = _stock(q, k, v, 0.125)
+    enable(FPV2Config(alpha=0, sink_tokens=0, window_tokens=0), min_tokens=1)
+    actual = _hook_call(q.to(cuda), k.to(cuda), v.to(cuda), 0.125)
+    assert F.scaled_dot_product_attention is not _ORIGINAL_SDPA
+    assert attention_errors(to_np(actual), expected)["rel"] < REL
+
+
+@pytest.mark.parametrize(("key_length", "query_length"),
+                         [(4096, 4096), (4100, 4100), (8192, 2048), (4100, 1000), (6000, 128)])
+def test_real_shape_alpha_zero_matches_stock(cuda, key_length, query_length):
+    # tests/test_patch.py:110-133
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn((1, 8, query_length, 128), generator=g).bfloat16()
+    k = torch.randn((1, 2, key_length, 128), generator=g).bfloat16()
+    v = torch.randn((1, 2, key_length, 128), generator=g).bfloat16()
+    expected = _stock(q, k, v, 128 ** -0.5)
+    enable(FPV2Config(alpha=0, sink_tokens=0, window_tokens=0), min_tokens=1)
+    actual = to_np(_hook_call(q.to(cuda), k.to(cuda), v.to(cuda), 128 ** -0.5))
+    err = attention_errors(actual, expected)
+    assert err["rel"] < REL and err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+@pytest.mark.parametrize(("length", "query_length", "kind"),
+                         [(64, 64, "causal"), (128, 1, "causal"), (128, 32, "causal"),
+                          (128, 128, "none"), (128, 128, "array")])
+def test_ineligible_calls_are_bit_identical(cuda, length, query_length, kind):
+    # tests/test_patch.py:76-107
+    q, k, v = (x.to(cuda) for x in _inputs(length, query_length))
+    kwargs = dict(scale=0.125, enable_gqa=True)
+    if kind == "causal":
+        kwargs["is_causal"] = True
+    elif kind == "array":
+        kwargs["attn_mask"] = torch.zeros((query_length, length), dtype=torch.bfloat16,
+                                          device=cuda)
+    expected = _ORIGINAL_SDPA(q, k, v, **kwargs)
+    enable(min_tokens=128)
+    actual = F.scaled_dot_product_attention(q, k, v, **kwargs)
+    assert torch.equal(actual, expected)
+
+
+def test_tile_aligned_chunks_match_single_shot_fpv2(cuda):
+    # tests/test_patch.py:136-166
+    q, k, v = structured_qkv(length=8192, query_heads=8, kv_heads=2, head_dim=128,
+                             dtype=torch.bfloat16, seed=23, device=cuda)
+    q, k, v = q[None], k[None], v[None]
+    config = FPV2Config(alpha=0.15, mean_correction=True)
+    scale = 128 ** -0.5
+    expected = fpv2_sdpa(q, k, v, scale=scale, config=config)
+    chunks = []
+    for end in range(2048, 8193, 2048):
+        cfg = _request_config(config, end, q.shape[-2])
+        chunks.append(fpv2_sdpa(q[:, :, end - 2048:end], k[:, :, :end], v[:, :, :end],
+                                scale=scale, config=cfg))
+    actual = torch.cat(chunks, dim=2)
+    assert attention_errors(to_np(actual), to_np(expected))["rel"] < 1e-2
+
+
+def test_block_sparsity_includes_dense_gated_prefill(cuda):
+    # tests/test_patch.py:180-201
+    q, k, v = (x.to(cuda) for x in _inputs(256))
+    enable(FPV2Config(alpha=1e9, sink_tokens=0, window_tokens=0, last_n_blocks=0),
+           min_tokens=256, collect_stats=True)
+    F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125, enable_gqa=True)
+    assert block_sparsity() == pytest.approx(1 / 3)
+    q, k, v = (x.to(cuda) for x in _inputs(128))
+    F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125, enable_gqa=True)
+    assert block_sparsity() == pytest.approx(1 / 4)
+
+
+def test_strided_model_layout_is_read_in_place(cuda):
+    """[B, L, H, D] activations transposed to [B, H, L, D] views (no copy)."""
+    g = torch.Generator().manual_seed(29)
+    x = torch.randn((1, 4096, 8 + 2 + 2, 128), generator=g).bfloat16().to(cuda)
+    q, k, v = (x[:, :, :8].transpose(1, 2), x[:, :, 8:10].transpose(1, 2),
+               x[:, :, 10:].transpose(1, 2))
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    a = fpv2_sdpa(q, k, v, scale=128 ** -0.5, config=config)
+    b = fpv2_sdpa(q.contiguous(), k.contiguous(), v.contiguous(), scale=128 ** -0.5,
+                  config=config)
+    assert torch.equal(a, b)
+
+
+def _baseline_parity(cuda, seq, planted, tiles):
+    q, k, v = baseline_qkv(seq, planted=planted, heavy_fraction=0.06, seed=0)
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    scale = 128 ** -0.5
+    enable(config, min_tokens=1, total_tokens=seq)
+    out = _hook_call(q[None].to(cuda), k[None].to(cuda), v[None].to(cuda), scale)[0]
+    want, plan = orc.fpv2_sdpa_oracle(to_np(q), to_np(k), to_np(v), scale=scale,
+                                      config=orc.OracleConfig(alpha=0.1, sink_tokens=128),
+                                      return_plan=True, tiles=tiles)
+    tq = plan["config"].tile_q
+    rows = np.concatenate([np.arange(t * tq, (t + 1) * tq) for t in tiles])
+    got = to_np(out)[:, rows]
+    err = attention_errors(got, want[:, rows])
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+    return plan
+
+
+def test_baseline_config1_8k_matches_oracle(cuda):
+    nt = 8192 // 32
+    tiles = sorted({0, 1, 2, 3, 100, 177, nt // 2, nt - 3, nt - 2, nt - 1})
+    _baseline_parity(cuda, 8192, 3.0, tiles)
+
+
+def test_baseline_contrast_variant_exercises_pruning(cuda):
+    nt = 8192 // 32
+    tiles = sorted({2, 40, 129, nt - 40, nt - 3, nt - 1})
+    plan = _baseline_parity(cuda, 8192, 3.0 * 128 ** 0.5, tiles)
+    dens = orc.density(plan["selected"], config=plan["config"])
+    assert dens < 0.6  # real pruning, so the pooled correction is active
+    assert int(plan["lists"][3].max()) > 0
