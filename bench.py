@@ -75,6 +75,26 @@ def retained_flops(keep, seq, torch):
     return 4 * D * group * (exact + corr), float(mask.float().mean().item())
 
 
+def profiled_traffic(seq: int, alpha: float):
+    """HBM bytes per launch of the attention kernel from the committed rocprofv3
+    summary of this workload (calibrated FETCH_SIZE + WRITE_SIZE), or None."""
+    path = ROOT / "profiles" / f"fpv2_layer_seq{seq}_alpha{alpha}.md"
+    if not path.exists():
+        return None, None
+    text = path.read_text()
+    start = text.find("## HBM traffic")
+    if start < 0:
+        return None, None
+    for line in text[start:].splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 6 and cells[0].startswith("`sparse_attn_kernel<fpv2::bf16_t, 128"):
+            try:
+                return float(cells[5]), str(path.relative_to(ROOT))
+            except ValueError:
+                return None, None
+    return None, None
+
+
 def dense_flops(seq: int) -> int:
     return 4 * D * HQ * seq * (seq + 1) // 2
 
@@ -221,6 +241,9 @@ def main(argv=None) -> int:
                          "high-contrast variant")
     ap.add_argument("--profile", action="store_true",
                     help="primary config only, no CPU baseline (for rocprofv3 runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES bytes (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters for the traffic figure)")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -235,6 +258,15 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        src = torch.empty(args.copy_calibration, dtype=torch.uint8, device="cuda:0")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.copy_calibration} bytes")
+        return 0
     from fpv2 import _lib
 
     _lib.load()
@@ -257,6 +289,7 @@ def main(argv=None) -> int:
         cpu = cpu_baseline(torch, data, args.seq, args.alpha, args.cpu_budget)
 
     attn_s = primary["stage_ms"]["attention"] * 1e-3
+    traffic, traffic_src = profiled_traffic(args.seq, args.alpha)
     line = {
         "metric": METRIC,
         "value": primary["retained_tflops_layer"],
@@ -295,7 +328,8 @@ def main(argv=None) -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": primary["retained_flops"] / attn_s / 1e12 / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
         },
         "cpu_baseline": cpu,
         **extra,
