@@ -129,9 +129,17 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     const uint32_t qoff =
         row_valid ? static_cast<uint32_t>((g * a.q_hs + static_cast<int64_t>(pos) * a.q_rs + hf * 8) * 2)
                   : kOOB;
+    // The softmax folds the scale into one FMA per logit and needs a positive
+    // factor: for scale < 0 the queries are negated instead (s*c = (-s)*(-c)).
+    const uint32_t sign = a.c_scale < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int k = 0; k < TL::KS; ++k) qf[k] = as_vec8<T>(buf_load16(qr, qoff + (row_valid ? k * 32 : 0)));
+    for (int k = 0; k < TL::KS; ++k) {
+      u32x4 v = buf_load16(qr, qoff + (row_valid ? k * 32 : 0));
+      v ^= sign;
+      qf[k] = as_vec8<T>(v);
+    }
   }
+  const float c_pos = fmaxf(fabsf(a.c_scale), 1e-30f);
 
   // ---- block lists of (h, t), clipped as kernel.py:555-558 ----
   const int Nb = a.Nb;
@@ -286,10 +294,15 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   };
 
   // ---- accumulators ----
+  // Online softmax in log2 units with a lazily updated reference max m_ref:
+  // P = exp2(s*c + shift - m_ref) may exceed 1 by up to 2^kRescaleSlack, and
+  // O / l are rescaled only when some row's max grows past that, so the
+  // common case costs no rescale at all.  The result O / l is unchanged.
+  constexpr float kRescaleSlack = 8.0f;
   f32x16 o[TL::DT];
 #pragma unroll
   for (int i = 0; i < TL::DT; ++i) o[i] = f32x16{};
-  float m_run = neg_inf();
+  float m_ref = neg_inf();
   float l_run = 0.f;
 
   auto compute_step = [&](const Step& s, int buf) {
@@ -305,31 +318,41 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         st[kt] = Elem<T>::mfma32(as_vec8<T>(kv), qf[k], st[kt]);
       }
     }
-    // scale to log2 units, shift pooled entries, mask
+    // mask (diagonal / partial sub-tiles only) and raw row max
     const bool sel = s.phase == kSel;
     const float shift = sel ? 0.f : a.shift;
     const bool need_mask = (s.nkeys < BN) || (sel && s.key0 + BN - 1 > abs_first);
-    const int key_lim = sel ? qpos_abs - s.key0 : BN;  // causal: e <= key_lim
     float mx = neg_inf();
+    if (need_mask) {
+      const int key_lim = sel ? qpos_abs - s.key0 : BN;  // causal: e <= key_lim
+#pragma unroll
+      for (int kt = 0; kt < TL::NTK; ++kt) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
+          st[kt][j] = (e < s.nkeys && e <= key_lim) ? st[kt][j] : neg_inf();
+        }
+      }
+    }
 #pragma unroll
     for (int kt = 0; kt < TL::NTK; ++kt) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float x = st[kt][j] * a.c_scale + shift;
-        if (need_mask) {
-          const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
-          x = (e < s.nkeys && e <= key_lim) ? x : neg_inf();
-        }
-        st[kt][j] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, st[kt][j]), st[kt][j + 1]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == neg_inf()) ? 0.f : m_new;
-    const float rescale = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    float lsum = 0.f;
+    const float m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
+    if (__ballot(m_cand > m_ref + kRescaleSlack) != 0ull) {
+      const float m_new = fmaxf(m_ref, m_cand);
+      const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      m_ref = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < TL::DT; ++dt) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
+      }
+    }
+    const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
     vec8 pb[TL::NTK][2];
 #pragma unroll
     for (int kt = 0; kt < TL::NTK; ++kt) {
@@ -338,19 +361,13 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         u32x4 w;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p0 = __builtin_amdgcn_exp2f(st[kt][u * 8 + 2 * i] - m_use);
-          const float p1 = __builtin_amdgcn_exp2f(st[kt][u * 8 + 2 * i + 1] - m_use);
-          lsum += p0 + p1;
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kt][u * 8 + 2 * i], c_pos, bias));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kt][u * 8 + 2 * i + 1], c_pos, bias));
           w[i] = pack2<T>(p0, p1);
+          l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
         }
         pb[kt][u] = as_vec8<T>(w);
       }
-    }
-    l_run = l_run * rescale + lsum;
-#pragma unroll
-    for (int dt = 0; dt < TL::DT; ++dt) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) o[dt][j] *= rescale;
     }
     // O^T += V^T . P^T
 #pragma unroll

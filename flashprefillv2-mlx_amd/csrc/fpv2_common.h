@@ -77,6 +77,21 @@ __device__ __forceinline__ uint32_t pack2<f16_t>(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// acc + lo(w) + hi(w) for two packed 16-bit elements of T
+// (v_dot2c_f32_bf16 / v_dot2_f32_f16 against (1, 1)).
+template <typename T>
+__device__ __forceinline__ float add_pair(uint32_t w, float acc);
+template <>
+__device__ __forceinline__ float add_pair<bf16_t>(uint32_t w, float acc) {
+  const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+}
+template <>
+__device__ __forceinline__ float add_pair<f16_t>(uint32_t w, float acc) {
+  const f16x2 one = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+}
+
 template <typename T>
 __device__ __forceinline__ typename Elem<T>::vec8 as_vec8(u32x4 v) {
   return __builtin_bit_cast(typename Elem<T>::vec8, v);

@@ -14,7 +14,8 @@ from pathlib import Path
 import torch
 
 LIB_NAME = "libfpv2_hip.so"
-LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+# The in-tree build; FPV2_LIBRARY may point at another build of the same ABI.
+LIB_PATH = Path(os.environ.get("FPV2_LIBRARY") or Path(__file__).resolve().parent / LIB_NAME)
 ABI_VERSION = 1
 
 FPV2_OK = 0
