@@ -32,6 +32,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kRows = 128;  // packed query rows per workgroup
 
+// gfx950 transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group
+// lane i receives element i%4 of the 8-byte chunks addressed by lanes
+// i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -51,16 +61,6 @@ struct AttnArgs {
   uint32_t q_bytes, k_bytes, v_bytes, pooled_bytes;  // descriptor ranges
 };
 
-enum Phase { kSel = 0, kCorr = 1, kDone = 2 };
-
-struct Step {
-  int phase;
-  int li;     // list index (selected phase) / first list entry (correction)
-  int sub;    // sub-tile within the block (selected phase)
-  int key0;   // first key of the sub-tile (selected phase)
-  int nkeys;  // valid keys in the sub-tile (selected) / entries (correction)
-};
-
 __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
@@ -71,20 +71,26 @@ template <int D> struct SubTile { static constexpr int BN = D <= 64 ? 64 : 32; }
 template <typename T, int D, bool CORR>
 struct AttnTile {
   static constexpr int BN = SubTile<D>::BN;     // keys per sub-tile
-  static constexpr int LDV = BN + 4;            // V^T row stride (elements)
-  static constexpr int LDK = D + 8;             // K row stride (elements)
+  static constexpr int LDK = D + 8;             // K row stride: conflict-free b128 row reads
+  static constexpr int LDVR = D + 32;           // V row stride: conflict-free transpose reads
   static constexpr int KS = D / 16;             // QK^T k-steps
   static constexpr int DT = D / 32;             // O^T row tiles (32 dims)
   static constexpr int NTK = BN / 32;           // S^T key tiles
-  static constexpr int DG = D / 8;              // 8-dim groups
-  static constexpr int KCHUNKS = BN * DG;       // 16-B K chunks per sub-tile
-  static constexpr int KTASK = (KCHUNKS + kThreads - 1) / kThreads;
-  static constexpr int DGP = (DG + 7) / 8 * 8;  // padded to whole 8-lane groups
-  static constexpr int VTASKS = (BN / 4) * DGP;
-  static constexpr int VT = (VTASKS + kThreads - 1) / kThreads;
+  static constexpr int DG = D / 8;              // 16-byte chunks per row
+  static constexpr int CHUNKS = BN * DG;        // 16-byte chunks per K (or V) sub-tile
+  static constexpr int TASKS = (CHUNKS + kThreads - 1) / kThreads;
   static constexpr int K_ELEMS = BN * LDK;
-  static constexpr int V_ELEMS = D * LDV;
+  static constexpr int V_ELEMS = BN * LDVR;
   static constexpr int STAGE = K_ELEMS + V_ELEMS;  // uint16 elements per stage
+};
+
+// One K/V sub-tile of the walk: `nkeys` valid rows starting at key `key0`
+// (exact phase) or at pruned-list entry `li` (correction phase).
+struct Step {
+  int corr;   // 0: exact keys of a selected block, 1: pooled entries of pruned blocks
+  int li;     // first pruned-list entry (correction)
+  int key0;   // first key (exact)
+  int nkeys;  // valid rows in the sub-tile
 };
 
 template <typename T, int D, bool CORR>
@@ -92,7 +98,6 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   using TL = AttnTile<T, D, CORR>;
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = TL::BN;
-  constexpr int LDV = TL::LDV;
   extern __shared__ __align__(16) uint16_t lds[];
 
   const int tid = threadIdx.x;
@@ -150,50 +155,48 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const int pr_count = CORR ? clampi(a.pcounts[list_row], 0, Nb) : 0;
   const int subs = (a.bk + BN - 1) / BN;
 
-  auto make_sel = [&](int li, int sub) -> Step {
-    const int blk = clampi(ids[li], 0, Nb - 1);
+  // The walk stops at the first listed block that starts after the tile's
+  // last row (kernel.py:252): find it with one ballot per 64 entries.
+  int li_end = sel_count;
+  for (int base = 0; base < sel_count; base += 64) {
+    const int li = base + lane;
+    const bool past = li < sel_count && clampi(ids[li], 0, Nb - 1) * a.bk > abs_last;
+    const uint64_t m = __ballot(past);
+    if (m != 0ull) {
+      li_end = base + static_cast<int>(__builtin_ctzll(m));
+      break;
+    }
+  }
+  // Exact-phase sub-tiles: every sub-tile of the blocks before li_end, the
+  // last block trimmed at the tile's last row; sub-tiles of other blocks that
+  // start past it (only in non-ascending lists) are skipped as empty.
+  int n_sel = 0;
+  if (li_end > 0) {
+    const int last_blk = clampi(ids[li_end - 1], 0, Nb - 1);
+    n_sel = (li_end - 1) * subs + min(subs, (abs_last - last_blk * a.bk) / BN + 1);
+  }
+  const int n_corr = CORR ? (pr_count + BN - 1) / BN : 0;
+  const int n_steps = n_sel + n_corr;
+
+  // Step descriptor for linear step `it` (uniform scalar arithmetic).
+  auto step_at = [&](int it) -> Step {
     Step s;
-    s.phase = kSel;
-    s.li = li;
-    s.sub = sub;
-    s.key0 = blk * a.bk + sub * BN;
-    const int n = min(min(a.bk - sub * BN, BN), a.Lk - s.key0);
-    s.nkeys = n < 0 ? 0 : n;
-    return s;
-  };
-  auto corr_start = [&]() -> Step {
-    Step s{kDone, 0, 0, 0, 0};
-    if (CORR && pr_count > 0) {
-      s.phase = kCorr;
-      s.nkeys = min(pr_count, BN);
+    if (it < n_sel) {
+      const int li = it / subs;
+      const int sub = it - li * subs;
+      s.corr = 0;
+      s.li = li;
+      s.key0 = clampi(ids[li], 0, Nb - 1) * a.bk + sub * BN;
+      int n = min(min(a.bk - sub * BN, BN), a.Lk - s.key0);
+      if (s.key0 > abs_last) n = 0;
+      s.nkeys = n < 0 ? 0 : n;
+    } else {
+      s.corr = 1;
+      s.li = (it - n_sel) * BN;
+      s.key0 = 0;
+      s.nkeys = min(pr_count - s.li, BN);
     }
     return s;
-  };
-  auto first_step = [&]() -> Step {
-    if (sel_count > 0) {
-      const Step s = make_sel(0, 0);
-      if (s.key0 <= abs_last) return s;
-    }
-    return corr_start();
-  };
-  auto advance = [&](const Step& c) -> Step {
-    if (c.phase == kSel) {
-      if (c.sub + 1 < subs) {
-        const Step s = make_sel(c.li, c.sub + 1);
-        if (s.key0 <= abs_last) return s;
-      }
-      if (c.li + 1 < sel_count) {
-        const Step s = make_sel(c.li + 1, 0);
-        if (s.key0 <= abs_last) return s;
-      }
-      return corr_start();
-    }
-    if (c.phase == kCorr && c.li + BN < pr_count) {
-      Step s{kCorr, c.li + BN, 0, 0, min(pr_count - c.li - BN, BN)};
-      return s;
-    }
-    Step d{kDone, 0, 0, 0, 0};
-    return d;
   };
 
   // ---- global -> register staging of one sub-tile (buffer loads) ----
@@ -201,94 +204,41 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
   const rsrc_t pkr = make_rsrc(a.pk + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
   const rsrc_t pvr = make_rsrc(a.pv + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
-  u32x4 kreg[TL::KTASK];
-  u32x4 vreg[TL::VT][4];
+  u32x4 kreg[TL::TASKS];
+  u32x4 vreg[TL::TASKS];
 
   auto load_step = [&](const Step& s) {
-    if (s.phase == kSel) {
 #pragma unroll
-      for (int i = 0; i < TL::KTASK; ++i) {
-        const int tau = tid + i * kThreads;
-        const int e = tau / TL::DG;
-        const int c = tau - e * TL::DG;
-        const uint32_t off = (tau < TL::KCHUNKS && e < s.nkeys)
-                                 ? static_cast<uint32_t>(((s.key0 + e) * a.k_rs + c * 8) * 2)
-                                 : kOOB;
-        kreg[i] = buf_load16(kr, off);
-      }
-#pragma unroll
-      for (int i = 0; i < TL::VT; ++i) {
-        const int tau = tid + i * kThreads;
-        const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
-        const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
-        const bool task_ok = tau < TL::VTASKS && dg < TL::DG;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int e = kg * 4 + r;
-          const uint32_t off = (task_ok && e < s.nkeys)
-                                   ? static_cast<uint32_t>(((s.key0 + e) * a.v_rs + dg * 8) * 2)
-                                   : kOOB;
-          vreg[i][r] = buf_load16(vr, off);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TL::KTASK; ++i) {
-        const int tau = tid + i * kThreads;
-        const int e = tau / TL::DG;
-        const int c = tau - e * TL::DG;
-        const bool ok = tau < TL::KCHUNKS && e < s.nkeys;
+    for (int i = 0; i < TL::TASKS; ++i) {
+      const int tau = tid + i * kThreads;
+      const int e = tau / TL::DG;
+      const int c = tau - e * TL::DG;
+      const bool ok = tau < TL::CHUNKS && e < s.nkeys;
+      if (!s.corr) {
+        const uint32_t koff = ok ? static_cast<uint32_t>(((s.key0 + e) * a.k_rs + c * 8) * 2) : kOOB;
+        const uint32_t voff = ok ? static_cast<uint32_t>(((s.key0 + e) * a.v_rs + c * 8) * 2) : kOOB;
+        kreg[i] = buf_load16(kr, koff);
+        vreg[i] = buf_load16(vr, voff);
+      } else {
         const int blk = clampi(pids[ok ? s.li + e : s.li], 0, Nb - 1);
         const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
         kreg[i] = buf_load16(pkr, off);
-      }
-#pragma unroll
-      for (int i = 0; i < TL::VT; ++i) {
-        const int tau = tid + i * kThreads;
-        const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
-        const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
-        const bool task_ok = tau < TL::VTASKS && dg < TL::DG;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int e = kg * 4 + r;
-          const bool ok = task_ok && e < s.nkeys;
-          const int blk = clampi(pids[ok ? s.li + e : s.li], 0, Nb - 1);
-          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + dg * 8) * 2) : kOOB;
-          vreg[i][r] = buf_load16(pvr, off);
-        }
+        vreg[i] = buf_load16(pvr, off);
       }
     }
   };
 
-  auto store_step = [&](int buf) {
-    uint16_t* ks = lds + buf * TL::STAGE;
-    uint16_t* vs = ks + TL::K_ELEMS;
+  auto store_step = [&](uint16_t* stage) {
+    uint16_t* ks = stage;
+    uint16_t* vs = stage + TL::K_ELEMS;
 #pragma unroll
-    for (int i = 0; i < TL::KTASK; ++i) {
+    for (int i = 0; i < TL::TASKS; ++i) {
       const int tau = tid + i * kThreads;
       const int e = tau / TL::DG;
       const int c = tau - e * TL::DG;
-      if (tau < TL::KCHUNKS) store16(ks + e * TL::LDK + c * 8, kreg[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < TL::VT; ++i) {
-      const int tau = tid + i * kThreads;
-      const int kg = (tau & 7) + 8 * ((tau >> 6) % (BN / 32));
-      const int dg = ((tau >> 3) & 7) + 8 * ((tau >> 6) / (BN / 32));
-      if (tau < TL::VTASKS && dg < TL::DG) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {  // dims 8dg + 2w, 8dg + 2w + 1
-          const uint32_t r0 = vreg[i][0][w], r1 = vreg[i][1][w];
-          const uint32_t r2 = vreg[i][2][w], r3 = vreg[i][3][w];
-          u32x2 lo, hi;
-          lo[0] = (r0 & 0xffffu) | (r1 << 16);
-          lo[1] = (r2 & 0xffffu) | (r3 << 16);
-          hi[0] = (r0 >> 16) | (r1 & 0xffff0000u);
-          hi[1] = (r2 >> 16) | (r3 & 0xffff0000u);
-          const int d = dg * 8 + 2 * w;
-          *reinterpret_cast<u32x2*>(vs + d * LDV + kg * 4) = lo;
-          *reinterpret_cast<u32x2*>(vs + (d + 1) * LDV + kg * 4) = hi;
-        }
+      if (tau < TL::CHUNKS) {
+        store16(ks + e * TL::LDK + c * 8, kreg[i]);
+        store16(vs + e * TL::LDVR + c * 8, vreg[i]);
       }
     }
   };
@@ -305,9 +255,15 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   float m_ref = neg_inf();
   float l_run = 0.f;
 
-  auto compute_step = [&](const Step& s, int buf) {
-    const uint16_t* ks = lds + buf * TL::STAGE;
-    const uint16_t* vs = ks + TL::K_ELEMS;
+  // Per-lane pieces of the transpose-read address of V^T fragments: lane j of
+  // a 16-lane group reads row (j/4) and columns 4*(j%4).. of a 4-key x 16-dim
+  // patch; the transpose hands lane i the 4 keys of dim d0 + i.
+  const int tr_row = (lane & 15) >> 2;
+  const int tr_col = (lane & 3) * 4 + ((lane >> 4) & 1) * 16;
+
+  auto compute_step = [&](const Step& s, const uint16_t* stage) {
+    const uint16_t* ks = stage;
+    const uint16_t* vs = stage + TL::K_ELEMS;
     f32x16 st[TL::NTK];
 #pragma unroll
     for (int kt = 0; kt < TL::NTK; ++kt) {
@@ -319,12 +275,10 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
       }
     }
     // mask (diagonal / partial sub-tiles only) and raw row max
-    const bool sel = s.phase == kSel;
-    const float shift = sel ? 0.f : a.shift;
-    const bool need_mask = (s.nkeys < BN) || (sel && s.key0 + BN - 1 > abs_first);
-    float mx = neg_inf();
+    const float shift = s.corr ? a.shift : 0.f;
+    const bool need_mask = (s.nkeys < BN) || (!s.corr && s.key0 + BN - 1 > abs_first);
     if (need_mask) {
-      const int key_lim = sel ? qpos_abs - s.key0 : BN;  // causal: e <= key_lim
+      const int key_lim = s.corr ? BN : qpos_abs - s.key0;  // causal: e <= key_lim
 #pragma unroll
       for (int kt = 0; kt < TL::NTK; ++kt) {
 #pragma unroll
@@ -334,6 +288,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         }
       }
     }
+    float mx = neg_inf();
 #pragma unroll
     for (int kt = 0; kt < TL::NTK; ++kt) {
 #pragma unroll
@@ -341,16 +296,13 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
-    if (__ballot(m_cand > m_ref + kRescaleSlack) != 0ull) {
+    const bool upd = __ballot(m_cand > m_ref + kRescaleSlack) != 0ull;
+    float alpha = 1.f;
+    if (upd) {
       const float m_new = fmaxf(m_ref, m_cand);
-      const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
       m_ref = m_new;
       l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < TL::DT; ++dt) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
-      }
     }
     const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
     vec8 pb[TL::NTK][2];
@@ -369,39 +321,68 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         pb[kt][u] = as_vec8<T>(w);
       }
     }
-    // O^T += V^T . P^T
-#pragma unroll
-    for (int dt = 0; dt < TL::DT; ++dt) {
-      const uint16_t* vrow = vs + (dt * 32 + l32) * LDV + hf * 4;
+    // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
+    // transposing LDS reads of the row-major V tile: keys
+    // 32kt + 16u + 4hf + {0..3} and the same + 8, matching the key order of
+    // this lane's P values.
+    auto pv = [&]() {
 #pragma unroll
       for (int kt = 0; kt < TL::NTK; ++kt) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const u32x2 x0 = *reinterpret_cast<const u32x2*>(vrow + kt * 32 + u * 16);
-          const u32x2 x1 = *reinterpret_cast<const u32x2*>(vrow + kt * 32 + u * 16 + 8);
-          const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
-          o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[kt][u], o[dt]);
+          const int key_base = kt * 32 + u * 16 + hf * 4 + tr_row;
+#pragma unroll
+          for (int dt = 0; dt < TL::DT; ++dt) {
+            const uint16_t* p0 = vs + key_base * TL::LDVR + dt * 32 + tr_col;
+            const u32x2 x0 = ds_read_tr16(p0);
+            const u32x2 x1 = ds_read_tr16(p0 + 8 * TL::LDVR);
+            const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
+            o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[kt][u], o[dt]);
+          }
         }
       }
+    };
+    if (upd) {
+#pragma unroll
+      for (int dt = 0; dt < TL::DT; ++dt) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
+      }
     }
+    pv();
   };
 
-  // ---- pipelined loop over sub-tiles ----
-  Step cur = first_step();
-  if (cur.phase != kDone) {
+  // ---- pipelined walk over the sub-tiles: prefetch step it+1 into
+  // registers while step it is multiplied from LDS; two LDS stages, the loop
+  // unrolled by two so each half uses a fixed stage ----
+  uint16_t* stage0 = lds;
+  uint16_t* stage1 = lds + TL::STAGE;
+  Step cur = step_at(0);
+  if (n_steps > 0) {
     load_step(cur);
-    store_step(0);
+    store_step(stage0);
   }
   __syncthreads();
-  int buf = 0;
-  while (cur.phase != kDone) {
-    const Step nxt = advance(cur);
-    if (nxt.phase != kDone) load_step(nxt);
-    compute_step(cur, buf);
-    if (nxt.phase != kDone) store_step(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
-    cur = nxt;
+  for (int it = 0; it < n_steps; it += 2) {
+    {
+      const bool more = it + 1 < n_steps;
+      const Step nxt = step_at(it + 1);
+      if (more) load_step(nxt);
+      compute_step(cur, stage0);
+      if (more) store_step(stage1);
+      __syncthreads();
+      cur = nxt;
+      if (!more) break;
+    }
+    {
+      const bool more = it + 2 < n_steps;
+      const Step nxt = step_at(it + 2);
+      if (more) load_step(nxt);
+      compute_step(cur, stage1);
+      if (more) store_step(stage0);
+      __syncthreads();
+      cur = nxt;
+    }
   }
 
   // ---- normalise and store ----
