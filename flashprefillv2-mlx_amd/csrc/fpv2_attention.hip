@@ -65,23 +65,33 @@ __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
 
-// Keys per LDS sub-tile: 64 where the registers allow it, 32 for wide heads.
-template <int D> struct SubTile { static constexpr int BN = D <= 64 ? 64 : 32; };
+// Keys per LDS sub-tile: 64, or 32 for the 256-wide heads (registers).
+template <int D> struct SubTile { static constexpr int BN = D <= 128 ? 64 : 32; };
 
+// LDS stage layout.  A stage holds one K and one V sub-tile, row-major with
+// padded rows, viewed as a linear array of 16-byte slots so that it can be
+// filled by buffer_load_dwordx4 ... lds (each wave instruction writes 64
+// consecutive slots, lane i -> slot base + i).  Pad slots are loaded from an
+// out-of-range offset (zeros).
 template <typename T, int D, bool CORR>
 struct AttnTile {
   static constexpr int BN = SubTile<D>::BN;     // keys per sub-tile
-  static constexpr int LDK = D + 8;             // K row stride: conflict-free b128 row reads
-  static constexpr int LDVR = D + 32;           // V row stride: conflict-free transpose reads
+  static constexpr int DG = D / 8;              // 16-byte chunks per row
+  static constexpr int SK = DG + 1;             // K row: D + 8 elements (conflict-free b128 reads)
+  static constexpr int SV = DG + 4;             // V row: D + 32 elements (conflict-free transpose reads)
+  static constexpr int LDK = SK * 8;
+  static constexpr int LDVR = SV * 8;
   static constexpr int KS = D / 16;             // QK^T k-steps
   static constexpr int DT = D / 32;             // O^T row tiles (32 dims)
   static constexpr int NTK = BN / 32;           // S^T key tiles
-  static constexpr int DG = D / 8;              // 16-byte chunks per row
-  static constexpr int CHUNKS = BN * DG;        // 16-byte chunks per K (or V) sub-tile
-  static constexpr int TASKS = (CHUNKS + kThreads - 1) / kThreads;
-  static constexpr int K_ELEMS = BN * LDK;
-  static constexpr int V_ELEMS = BN * LDVR;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;  // uint16 elements per stage
+  static constexpr int K_INSTR = (BN * SK + 63) / 64;  // wave instructions per K sub-tile
+  static constexpr int V_INSTR = (BN * SV + 63) / 64;
+  static constexpr int K_ELEMS = K_INSTR * 64 * 8;     // uint16 elements
+  static constexpr int V_ELEMS = V_INSTR * 64 * 8;
+  static constexpr int STAGE = K_ELEMS + V_ELEMS;
+  static constexpr int WAVES = kThreads / 64;
+  static constexpr int KI_PER_WAVE = (K_INSTR + WAVES - 1) / WAVES;
+  static constexpr int VI_PER_WAVE = (V_INSTR + WAVES - 1) / WAVES;
 };
 
 // One K/V sub-tile of the walk: `nkeys` valid rows starting at key `key0`
@@ -98,11 +108,14 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   using TL = AttnTile<T, D, CORR>;
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = TL::BN;
-  extern __shared__ __align__(16) uint16_t lds[];
+  // Two LDS stages as separate objects, so stage reads and the asynchronous
+  // fills of the other stage are known not to alias.
+  __shared__ __align__(1024) uint16_t stage0[TL::STAGE];
+  __shared__ __align__(1024) uint16_t stage1[TL::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int hf = lane >> 5;
 
@@ -199,48 +212,116 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     return s;
   };
 
-  // ---- global -> register staging of one sub-tile (buffer loads) ----
+  // ---- global -> LDS fills (buffer_load_dwordx4 ... lds) ----
+  // Per lane and per wave instruction: the slot's row and its byte offset
+  // within the row pattern (kOOB for pad slots).  Constant over the walk.
   const rsrc_t kr = make_rsrc(a.k + h * a.k_hs, a.k_bytes);
   const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
   const rsrc_t pkr = make_rsrc(a.pk + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
   const rsrc_t pvr = make_rsrc(a.pv + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
-  u32x4 kreg[TL::TASKS];
-  u32x4 vreg[TL::TASKS];
-
-  auto load_step = [&](const Step& s) {
+  // Per lane and wave instruction, the byte offset of the slot within a
+  // sub-tile of consecutive rows (-1 for pad slots); rows are recomputed only
+  // on the rare partial and correction sub-tiles.
+  int k_pre[TL::KI_PER_WAVE], v_pre[TL::VI_PER_WAVE];
 #pragma unroll
-    for (int i = 0; i < TL::TASKS; ++i) {
-      const int tau = tid + i * kThreads;
-      const int e = tau / TL::DG;
-      const int c = tau - e * TL::DG;
-      const bool ok = tau < TL::CHUNKS && e < s.nkeys;
-      if (!s.corr) {
-        const uint32_t koff = ok ? static_cast<uint32_t>(((s.key0 + e) * a.k_rs + c * 8) * 2) : kOOB;
-        const uint32_t voff = ok ? static_cast<uint32_t>(((s.key0 + e) * a.v_rs + c * 8) * 2) : kOOB;
-        kreg[i] = buf_load16(kr, koff);
-        vreg[i] = buf_load16(vr, voff);
-      } else {
-        const int blk = clampi(pids[ok ? s.li + e : s.li], 0, Nb - 1);
-        const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
-        kreg[i] = buf_load16(pkr, off);
-        vreg[i] = buf_load16(pvr, off);
+  for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
+    const int slot = (wave + i * TL::WAVES) * 64 + lane;
+    const int r = slot / TL::SK, c = slot - r * TL::SK;
+    k_pre[i] = (c < TL::DG && r < BN) ? (r * a.k_rs + c * 8) * 2 : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
+    const int slot = (wave + i * TL::WAVES) * 64 + lane;
+    const int r = slot / TL::SV, c = slot - r * TL::SV;
+    v_pre[i] = (c < TL::DG && r < BN) ? (r * a.v_rs + c * 8) * 2 : -1;
+  }
+
+  // One K/V fill of `stage` for step s.  `rows_of` gives the slot's row
+  // (BN for pad slots) and its 16-byte chunk.
+  auto slot_of = [&](int j, int per_row, int& row, int& chunk) {
+    const int slot = j * 64 + lane;
+    row = slot / per_row;
+    chunk = slot - row * per_row;
+    if (chunk >= TL::DG || row >= BN) row = BN;
+  };
+  auto fill_step = [&](const Step& s, uint16_t* stage) {
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    if (!s.corr && s.nkeys == BN) {  // full exact sub-tile: offsets only
+      const int kbase = s.key0 * a.k_rs * 2;
+      const int vbase = s.key0 * a.v_rs * 2;
+#pragma unroll
+      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::K_INSTR) {
+          const uint32_t off = k_pre[i] >= 0 ? static_cast<uint32_t>(kbase + k_pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::V_INSTR) {
+          const uint32_t off = v_pre[i] >= 0 ? static_cast<uint32_t>(vbase + v_pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
+                                                   off, 0, 0, 0);
+        }
+      }
+    } else if (!s.corr) {  // partial exact sub-tile (end of the keys / of the block)
+      const int kbase = s.key0 * a.k_rs * 2;
+      const int vbase = s.key0 * a.v_rs * 2;
+#pragma unroll
+      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::K_INSTR) {
+          int row, chunk;
+          slot_of(j, TL::SK, row, chunk);
+          const uint32_t off = row < s.nkeys ? static_cast<uint32_t>(kbase + k_pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::V_INSTR) {
+          int row, chunk;
+          slot_of(j, TL::SV, row, chunk);
+          const uint32_t off = row < s.nkeys ? static_cast<uint32_t>(vbase + v_pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
+                                                   off, 0, 0, 0);
+        }
+      }
+    } else {  // correction: gather pooled rows of the pruned blocks
+#pragma unroll
+      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::K_INSTR) {
+          int row, chunk;
+          slot_of(j, TL::SK, row, chunk);
+          const bool ok = row < s.nkeys;
+          const int blk = clampi(pids[ok ? s.li + row : s.li], 0, Nb - 1);
+          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + chunk * 8) * 2) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
+        const int j = wave + i * TL::WAVES;
+        if (j < TL::V_INSTR) {
+          int row, chunk;
+          slot_of(j, TL::SV, row, chunk);
+          const bool ok = row < s.nkeys;
+          const int blk = clampi(pids[ok ? s.li + row : s.li], 0, Nb - 1);
+          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + chunk * 8) * 2) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(pvr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
+                                                   off, 0, 0, 0);
+        }
       }
     }
   };
-
-  auto store_step = [&](uint16_t* stage) {
-    uint16_t* ks = stage;
-    uint16_t* vs = stage + TL::K_ELEMS;
-#pragma unroll
-    for (int i = 0; i < TL::TASKS; ++i) {
-      const int tau = tid + i * kThreads;
-      const int e = tau / TL::DG;
-      const int c = tau - e * TL::DG;
-      if (tau < TL::CHUNKS) {
-        store16(ks + e * TL::LDK + c * 8, kreg[i]);
-        store16(vs + e * TL::LDVR + c * 8, vreg[i]);
-      }
-    }
+  // Wait for this wave's outstanding fills (vmcnt = 0), then for all waves.
+  auto fills_done = [&]() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
+    __syncthreads();
   };
 
   // ---- accumulators ----
@@ -261,39 +342,33 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const int tr_row = (lane & 15) >> 2;
   const int tr_col = (lane & 3) * 4 + ((lane >> 4) & 1) * 16;
 
-  auto compute_step = [&](const Step& s, const uint16_t* stage) {
+  // One 32-key slice (key tile kt of the sub-tile): S^T, mask, online softmax
+  // update, P, then O^T += V^T . P^T.  Slicing the 64-key sub-tile keeps only
+  // 16 S and 8 P registers live.
+  auto compute_slice = [&](const Step& s, const uint16_t* stage, int kt) {
     const uint16_t* ks = stage;
     const uint16_t* vs = stage + TL::K_ELEMS;
-    f32x16 st[TL::NTK];
+    f32x16 st = f32x16{};
 #pragma unroll
-    for (int kt = 0; kt < TL::NTK; ++kt) {
-      st[kt] = f32x16{};
-#pragma unroll
-      for (int k = 0; k < TL::KS; ++k) {
-        const u32x4 kv = load16(ks + (kt * 32 + l32) * TL::LDK + k * 16 + hf * 8);
-        st[kt] = Elem<T>::mfma32(as_vec8<T>(kv), qf[k], st[kt]);
-      }
+    for (int k = 0; k < TL::KS; ++k) {
+      const u32x4 kv = load16(ks + (kt * 32 + l32) * TL::LDK + k * 16 + hf * 8);
+      st = Elem<T>::mfma32(as_vec8<T>(kv), qf[k], st);
     }
+    __builtin_amdgcn_sched_barrier(0);
     // mask (diagonal / partial sub-tiles only) and raw row max
     const float shift = s.corr ? a.shift : 0.f;
-    const bool need_mask = (s.nkeys < BN) || (!s.corr && s.key0 + BN - 1 > abs_first);
+    const bool need_mask = (s.nkeys < (kt + 1) * 32) || (!s.corr && s.key0 + kt * 32 + 31 > abs_first);
     if (need_mask) {
       const int key_lim = s.corr ? BN : qpos_abs - s.key0;  // causal: e <= key_lim
 #pragma unroll
-      for (int kt = 0; kt < TL::NTK; ++kt) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
-          st[kt][j] = (e < s.nkeys && e <= key_lim) ? st[kt][j] : neg_inf();
-        }
+      for (int j = 0; j < 16; ++j) {
+        const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
+        st[j] = (e < s.nkeys && e <= key_lim) ? st[j] : neg_inf();
       }
     }
     float mx = neg_inf();
 #pragma unroll
-    for (int kt = 0; kt < TL::NTK; ++kt) {
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, st[kt][j]), st[kt][j + 1]);
-    }
+    for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, st[j]), st[j + 1]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
     const bool upd = __ballot(m_cand > m_ref + kRescaleSlack) != 0ull;
@@ -305,43 +380,19 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
       l_run *= alpha;
     }
     const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
-    vec8 pb[TL::NTK][2];
+    vec8 pb[2];
 #pragma unroll
-    for (int kt = 0; kt < TL::NTK; ++kt) {
+    for (int u = 0; u < 2; ++u) {
+      u32x4 w;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        u32x4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kt][u * 8 + 2 * i], c_pos, bias));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kt][u * 8 + 2 * i + 1], c_pos, bias));
-          w[i] = pack2<T>(p0, p1);
-          l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
-        }
-        pb[kt][u] = as_vec8<T>(w);
+      for (int i = 0; i < 4; ++i) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[u * 8 + 2 * i], c_pos, bias));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[u * 8 + 2 * i + 1], c_pos, bias));
+        w[i] = pack2<T>(p0, p1);
+        l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
       }
+      pb[u] = as_vec8<T>(w);
     }
-    // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
-    // transposing LDS reads of the row-major V tile: keys
-    // 32kt + 16u + 4hf + {0..3} and the same + 8, matching the key order of
-    // this lane's P values.
-    auto pv = [&]() {
-#pragma unroll
-      for (int kt = 0; kt < TL::NTK; ++kt) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int key_base = kt * 32 + u * 16 + hf * 4 + tr_row;
-#pragma unroll
-          for (int dt = 0; dt < TL::DT; ++dt) {
-            const uint16_t* p0 = vs + key_base * TL::LDVR + dt * 32 + tr_col;
-            const u32x2 x0 = ds_read_tr16(p0);
-            const u32x2 x1 = ds_read_tr16(p0 + 8 * TL::LDVR);
-            const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
-            o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[kt][u], o[dt]);
-          }
-        }
-      }
-    };
     if (upd) {
 #pragma unroll
       for (int dt = 0; dt < TL::DT; ++dt) {
@@ -349,38 +400,53 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
       }
     }
-    pv();
+    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
+    // transposing LDS reads of the row-major V tile: keys
+    // 32kt + 16u + 4hf + {0..3} and the same + 8, matching the key order of
+    // this lane's P values.
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int key_base = kt * 32 + u * 16 + hf * 4 + tr_row;
+#pragma unroll
+      for (int dt = 0; dt < TL::DT; ++dt) {
+        const uint16_t* p0 = vs + key_base * TL::LDVR + dt * 32 + tr_col;
+        const u32x2 x0 = ds_read_tr16(p0);
+        const u32x2 x1 = ds_read_tr16(p0 + 8 * TL::LDVR);
+        const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
+        o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
+      }
+    }
+  };
+  auto compute_step = [&](const Step& s, const uint16_t* stage) {
+#pragma unroll
+    for (int kt = 0; kt < TL::NTK; ++kt) {
+      if (kt * 32 < s.nkeys || kt == 0) compute_slice(s, stage, kt);
+    }
   };
 
-  // ---- pipelined walk over the sub-tiles: prefetch step it+1 into
-  // registers while step it is multiplied from LDS; two LDS stages, the loop
-  // unrolled by two so each half uses a fixed stage ----
-  uint16_t* stage0 = lds;
-  uint16_t* stage1 = lds + TL::STAGE;
+  // ---- pipelined walk over the sub-tiles: the fills of step it+1 run while
+  // step it is multiplied from the other stage; the loop is unrolled by two
+  // so each half uses a fixed stage ----
   Step cur = step_at(0);
-  if (n_steps > 0) {
-    load_step(cur);
-    store_step(stage0);
-  }
-  __syncthreads();
+  if (n_steps > 0) fill_step(cur, stage0);
+  fills_done();
   for (int it = 0; it < n_steps; it += 2) {
     {
       const bool more = it + 1 < n_steps;
       const Step nxt = step_at(it + 1);
-      if (more) load_step(nxt);
+      if (more) fill_step(nxt, stage1);
       compute_step(cur, stage0);
-      if (more) store_step(stage1);
-      __syncthreads();
+      fills_done();
       cur = nxt;
       if (!more) break;
     }
     {
       const bool more = it + 2 < n_steps;
       const Step nxt = step_at(it + 2);
-      if (more) load_step(nxt);
+      if (more) fill_step(nxt, stage0);
       compute_step(cur, stage1);
-      if (more) store_step(stage0);
-      __syncthreads();
+      fills_done();
       cur = nxt;
     }
   }
@@ -405,16 +471,10 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
 
 template <typename T, int D, bool CORR>
 int launch_attn(const AttnArgs& a, hipStream_t stream) {
-  using TL = AttnTile<T, D, CORR>;
-  const size_t lds = 2 * TL::STAGE * sizeof(uint16_t);
   auto kernel = sparse_attn_kernel<T, D, CORR>;
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                          static_cast<int>(lds)) != hipSuccess)
-    return fail(FPV2_ERR_LAUNCH, "sparse_attention: hipFuncSetAttribute failed");
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
   if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, stream, a);
   return check_launch("sparse_attention");
 }
 
