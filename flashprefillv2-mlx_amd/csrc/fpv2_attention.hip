@@ -24,6 +24,8 @@
 //   * grid order puts the KV head in the low bits of the workgroup id, so the
 //     round-robin dispatch over the 8 XCDs keeps one head per XCD L2 (for
 //     Hkv = 8), and tiles run latest (longest) first.
+#include <type_traits>
+
 #include "fpv2_common.h"
 
 namespace fpv2 {
@@ -35,12 +37,44 @@ constexpr int kRows = 128;  // packed query rows per workgroup
 // gfx950 transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group
 // lane i receives element i%4 of the 8-byte chunks addressed by lanes
 // i/4, i/4+4, i/4+8, i/4+12.
-__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(u32x2, v);
+//
+// Issued as inline asm on purpose: the compiler cannot tell this read from
+// the asynchronous global->LDS fills of the other stage and would otherwise
+// wait for those fills before the first such read of every step, which
+// serialises the fill latency with most of the step's work.  The result is
+// only valid after tr_wait() (s_waitcnt lgkmcnt(0)), which takes the result
+// registers as operands so their uses cannot be scheduled before it.  The
+// stage read here was completed by fills_done() (vmcnt(0) + barrier).
+template <int OFF>
+__device__ __forceinline__ u32x2 tr_read(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
 }
+template <int N>
+__device__ __forceinline__ void tr_wait(u32x2 (&r)[N]) {
+  static_assert(N == 8, "tr_wait ties a batch of 8 reads");
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                 "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+}
+__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(p)));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
+template <int I, int N>
+struct StaticFor {
+  template <typename F>
+  static __device__ __forceinline__ void run(F&& f) {
+    if constexpr (I < N) {
+      f(std::integral_constant<int, I>{});
+      StaticFor<I + 1, N>::run(f);
+    }
+  }
+};
 
 struct AttnArgs {
   const uint16_t* q;
@@ -191,18 +225,32 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const int n_corr = CORR ? (pr_count + BN - 1) / BN : 0;
   const int n_steps = n_sel + n_corr;
 
-  // Step descriptor for linear step `it` (uniform scalar arithmetic).
-  auto step_at = [&](int it) -> Step {
+  // Block ids of the selected list are read 64 at a time into one VGPR (lane
+  // = list entry) and handed out with readlane, so producing a step costs no
+  // memory round trip.  The walk state (list entry, sub-tile) advances
+  // incrementally.
+  int ids_base = 0;
+  int ids_lanes = lane < sel_count ? clampi(ids[lane], 0, Nb - 1) : 0;
+  int cur_li = 0, cur_sub = 0;
+  auto next_step = [&](int it) -> Step {
     Step s;
     if (it < n_sel) {
-      const int li = it / subs;
-      const int sub = it - li * subs;
+      if (cur_li - ids_base >= 64) {
+        ids_base += 64;
+        const int li = ids_base + lane;
+        ids_lanes = li < sel_count ? clampi(ids[li], 0, Nb - 1) : 0;
+      }
+      const int blk = __builtin_amdgcn_readlane(ids_lanes, cur_li - ids_base);
       s.corr = 0;
-      s.li = li;
-      s.key0 = clampi(ids[li], 0, Nb - 1) * a.bk + sub * BN;
-      int n = min(min(a.bk - sub * BN, BN), a.Lk - s.key0);
+      s.li = cur_li;
+      s.key0 = blk * a.bk + cur_sub * BN;
+      int n = min(min(a.bk - cur_sub * BN, BN), a.Lk - s.key0);
       if (s.key0 > abs_last) n = 0;
       s.nkeys = n < 0 ? 0 : n;
+      if (++cur_sub == subs) {
+        cur_sub = 0;
+        ++cur_li;
+      }
     } else {
       s.corr = 1;
       s.li = (it - n_sel) * BN;
@@ -404,19 +452,50 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
     // transposing LDS reads of the row-major V tile: keys
     // 32kt + 16u + 4hf + {0..3} and the same + 8, matching the key order of
-    // this lane's P values.
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int key_base = kt * 32 + u * 16 + hf * 4 + tr_row;
-#pragma unroll
-      for (int dt = 0; dt < TL::DT; ++dt) {
-        const uint16_t* p0 = vs + key_base * TL::LDVR + dt * 32 + tr_col;
-        const u32x2 x0 = ds_read_tr16(p0);
-        const u32x2 x1 = ds_read_tr16(p0 + 8 * TL::LDVR);
-        const u32x4 av = {x0[0], x0[1], x1[0], x1[1]};
-        o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-      }
-    }
+    // this lane's P values.  Reads go in batches of 8 (4 MFMA operands): the
+    // second batch is in flight while the first batch's MFMAs run.
+    constexpr int PV_OPS = 2 * TL::DT;  // MFMAs of this slice: (u, dt)
+    constexpr int PER_BATCH = 4;
+    constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
+    // lane part of the address; the (kt, u, dt, +8 keys) parts are immediates
+    const uint32_t vbase = lds_addr(vs) + ((hf * 4 + tr_row) * TL::LDVR + tr_col) * 2;
+    u32x2 rb[2][8];
+    auto issue_batch = [&](auto bc, u32x2 (&r)[8]) {
+      constexpr int b = decltype(bc)::value;
+      StaticFor<0, PER_BATCH>::run([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        constexpr int op = b * PER_BATCH + q;
+        if constexpr (op < PV_OPS) {
+          constexpr int u = op / TL::DT, dt = op % TL::DT;
+          constexpr int off = ((u * 16) * TL::LDVR + dt * 32) * 2;
+          r[2 * q] = tr_read<off>(vbase + kt * 32 * TL::LDVR * 2);
+          r[2 * q + 1] = tr_read<off + 8 * TL::LDVR * 2>(vbase + kt * 32 * TL::LDVR * 2);
+        } else {
+          r[2 * q] = u32x2{0u, 0u};
+          r[2 * q + 1] = u32x2{0u, 0u};
+        }
+      });
+    };
+    auto run_batch = [&](auto bc, u32x2 (&r)[8]) {
+      constexpr int b = decltype(bc)::value;
+      StaticFor<0, PER_BATCH>::run([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        constexpr int op = b * PER_BATCH + q;
+        if constexpr (op < PV_OPS) {
+          constexpr int u = op / TL::DT, dt = op % TL::DT;
+          const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
+          o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
+        }
+      });
+    };
+    issue_batch(std::integral_constant<int, 0>{}, rb[0]);
+    tr_wait(rb[0]);
+    StaticFor<0, BATCHES>::run([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      if constexpr (b + 1 < BATCHES) issue_batch(std::integral_constant<int, b + 1>{}, rb[(b + 1) & 1]);
+      run_batch(bc, rb[b & 1]);
+      if constexpr (b + 1 < BATCHES) tr_wait(rb[(b + 1) & 1]);
+    });
   };
   auto compute_step = [&](const Step& s, const uint16_t* stage) {
 #pragma unroll
@@ -428,14 +507,17 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   // ---- pipelined walk over the sub-tiles: the fills of step it+1 run while
   // step it is multiplied from the other stage; the loop is unrolled by two
   // so each half uses a fixed stage ----
-  Step cur = step_at(0);
+  Step cur = next_step(0);
   if (n_steps > 0) fill_step(cur, stage0);
   fills_done();
   for (int it = 0; it < n_steps; it += 2) {
     {
       const bool more = it + 1 < n_steps;
-      const Step nxt = step_at(it + 1);
-      if (more) fill_step(nxt, stage1);
+      Step nxt{};
+      if (more) {
+        nxt = next_step(it + 1);
+        fill_step(nxt, stage1);
+      }
       compute_step(cur, stage0);
       fills_done();
       cur = nxt;
@@ -443,8 +525,11 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     }
     {
       const bool more = it + 2 < n_steps;
-      const Step nxt = step_at(it + 2);
-      if (more) fill_step(nxt, stage0);
+      Step nxt{};
+      if (more) {
+        nxt = next_step(it + 2);
+        fill_step(nxt, stage0);
+      }
       compute_step(cur, stage1);
       fills_done();
       cur = nxt;
