@@ -67,15 +67,43 @@ def _compile(src: str, obj: Path, verbose: bool) -> None:
         print(msgs, flush=True)
 
 
+# Sources whose device assembly must pass check_isa (asm LDS reads).
+CHECKED = ["fpv2_attention.hip"]
+
+
+def _check_isa(src: str, tmp: Path, verbose: bool) -> None:
+    """Compile `src` to gfx950 assembly and run the async-LDS-read check."""
+    asm = tmp / (Path(src).stem + ".s")
+    cmd = [hipcc(), *compile_flags(), "--cuda-device-only", "-S", str(CSRC / src), "-o", str(asm)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src}:\n{res.stdout}{res.stderr}")
+    sys.path.insert(0, str(HERE))
+    try:
+        import check_isa
+    finally:
+        sys.path.pop(0)
+    errors = check_isa.check_text(asm.read_text())
+    if errors:
+        raise RuntimeError(f"{src}: asynchronous LDS read check failed "
+                           f"({len(errors)} violations):\n" + "\n".join(errors[:20]))
+    if verbose:
+        print(f"{src}: async LDS reads ok", flush=True)
+
+
 def build(jobs: int = 4, verbose: bool = False) -> Path:
     tmp = Path(tempfile.mkdtemp(prefix="fpv2_build_"))
     try:
         objs = [tmp / (Path(s).stem + ".o") for s in SOURCES]
+        tasks = [lambda so=so: _compile(so[0], so[1], verbose) for so in zip(SOURCES, objs)]
+        tasks += [lambda src=src: _check_isa(src, tmp, verbose) for src in CHECKED]
         with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
-            list(pool.map(lambda so: _compile(so[0], so[1], verbose), zip(SOURCES, objs)))
+            list(pool.map(lambda f: f(), tasks))
         tmp_out = OUT.with_suffix(".so.tmp")
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs),
-               "-o", str(tmp_out)]
+        # --no-undefined: a kernel whose host stub was not emitted must fail
+        # here, not at load time.
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined",
+               *map(str, objs), "-o", str(tmp_out)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")

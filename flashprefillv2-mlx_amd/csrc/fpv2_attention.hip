@@ -8,19 +8,22 @@
 // a +log2(block_k) logit shift; O /= l at the end.
 //
 // MI355X mapping:
-//   * one workgroup = one (KV head, query tile, 128-row chunk); the tile's
-//     G*tile_q packed rows (row = g*tile_q + p) share the block lists, so the
-//     G query heads of a KV head share every K/V load (the hook's tile is
-//     128 packed rows: one chunk);
-//   * 4 waves x 32 rows; Q lives in VGPRs for the whole workgroup;
+//   * one workgroup = one (KV head, query tile, row chunk); the tile's G*tile_q
+//     packed rows (row = g*tile_q + p) share the block lists, so the G query
+//     heads of a KV head share every K/V load.  A workgroup has WAVES = 8
+//     waves (256 rows, one workgroup per CU) when the packed rows come in
+//     multiples of 256, else 4 waves (128 rows);
+//   * each wave owns 32 query rows; Q lives in VGPRs for the whole walk;
 //   * S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: lane l owns query
 //     row l%32 and 16 of the 32 keys of each key tile, so row max/sum need a
 //     single lane-pair exchange and P feeds the next MFMA without a transpose;
 //   * O^T = V^T . P^T: the rescale by exp2(m_old - m_new) is lane-local;
-//   * K/V sub-tiles of 64 keys are double-buffered in LDS: the next sub-tile's
-//     global loads are in flight while the current one is multiplied; V is
-//     transposed on its way into LDS so both MFMA operands are 8-byte/16-byte
-//     LDS reads; row strides are padded against bank conflicts;
+//   * K/V sub-tiles (64 keys, 32 for D = 256) stream through a ring of NST
+//     LDS stages filled by buffer_load_dwordx4 ... lds, NST-1 sub-tiles ahead
+//     of the multiply; LDS rows are unpadded with an XOR swizzle of their
+//     16-byte chunks, so K (ds_read_b128) and V (ds_read_b64_tr_b16, which
+//     transposes on the way out) are read without bank conflicts and every
+//     wave issues the same number of fills per stage;
 //   * grid order puts the KV head in the low bits of the workgroup id, so the
 //     round-robin dispatch over the 8 XCDs keeps one head per XCD L2 (for
 //     Hkv = 8), and tiles run latest (longest) first.
@@ -31,37 +34,96 @@
 namespace fpv2 {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kRows = 128;  // packed query rows per workgroup
-
-// gfx950 transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group
+// ---- LDS access by inline asm ----
+// Every LDS read of the walk is inline asm.  The compiler cannot tell these
+// reads from the asynchronous global->LDS fills of other stages and would
+// otherwise wait for all outstanding fills before each stage's first read,
+// which serialises the fill latency with the multiply.  Reads complete in
+// order; a read's result is valid after lgkm_wait<N>() (s_waitcnt
+// lgkmcnt(N)) with N no larger than the number of LDS reads issued after it.
+// The wait takes the result registers as operands so that their uses cannot
+// be scheduled before it.  A stage is read only after the fills_done() wait
+// and barrier that completed its fills.
+//
+// With ASM = false (used where register pressure is high enough that the
+// compiler might spill or copy a register between the asm read and its
+// wait) the same reads are ordinary LDS loads and the transposing-read
+// builtin, and the compiler places the waits; the waits below are then
+// no-ops.
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+template <bool ASM, int OFF>
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+  if constexpr (ASM) {
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+  } else {
+    return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr + OFF));
+  }
+}
+// gfx950 transposing read (ds_read_b64_tr_b16): within each 16-lane group
 // lane i receives element i%4 of the 8-byte chunks addressed by lanes
 // i/4, i/4+4, i/4+8, i/4+12.
-//
-// Issued as inline asm on purpose: the compiler cannot tell this read from
-// the asynchronous global->LDS fills of the other stage and would otherwise
-// wait for those fills before the first such read of every step, which
-// serialises the fill latency with most of the step's work.  The result is
-// only valid after tr_wait() (s_waitcnt lgkmcnt(0)), which takes the result
-// registers as operands so their uses cannot be scheduled before it.  The
-// stage read here was completed by fills_done() (vmcnt(0) + barrier).
-template <int OFF>
-__device__ __forceinline__ u32x2 tr_read(uint32_t addr) {
+template <bool ASM, int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr(uint32_t addr) {
   static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
-  u32x2 r;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-  return r;
+  if constexpr (ASM) {
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+  } else {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        reinterpret_cast<lds_s16x4*>(static_cast<uintptr_t>(addr + OFF)));
+    return __builtin_bit_cast(u32x2, v);
+  }
+}
+template <bool ASM, int N>
+__device__ __forceinline__ void lgkm_wait(u32x4& r) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
+  if constexpr (ASM) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+template <bool ASM, int N>
+__device__ __forceinline__ void lgkm_wait(u32x2 (&r)[8]) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
+  if constexpr (ASM)
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
+                   "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+                 : "i"(N));
 }
 template <int N>
-__device__ __forceinline__ void tr_wait(u32x2 (&r)[N]) {
-  static_assert(N == 8, "tr_wait ties a batch of 8 reads");
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
-                 "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  // vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
-__device__ __forceinline__ uint32_t lds_addr(const uint16_t* p) {
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint16_t*)(p)));
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+// In-place multiply; keeps a conditionally rescaled MFMA accumulator in its
+// registers instead of a copy per branch.
+__device__ __forceinline__ void scale_in_place(f32x16& acc, float f) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    float x = acc[j];
+    asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(f));
+    acc[j] = x;
+  }
+}
+
+// max / sum of x over the lane pair (l, l ^ 32), one v_permlane32_swap_b32:
+// the two halves of the swap hold x of both lanes of the pair in either order.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
@@ -99,33 +161,30 @@ __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
 
-// Keys per LDS sub-tile: 64, or 32 for the 256-wide heads (registers).
-template <int D> struct SubTile { static constexpr int BN = D <= 128 ? 64 : 32; };
-
-// LDS stage layout.  A stage holds one K and one V sub-tile, row-major with
-// padded rows, viewed as a linear array of 16-byte slots so that it can be
-// filled by buffer_load_dwordx4 ... lds (each wave instruction writes 64
-// consecutive slots, lane i -> slot base + i).  Pad slots are loaded from an
-// out-of-range offset (zeros).
-template <typename T, int D, bool CORR>
-struct AttnTile {
-  static constexpr int BN = SubTile<D>::BN;     // keys per sub-tile
-  static constexpr int DG = D / 8;              // 16-byte chunks per row
-  static constexpr int SK = DG + 1;             // K row: D + 8 elements (conflict-free b128 reads)
-  static constexpr int SV = DG + 4;             // V row: D + 32 elements (conflict-free transpose reads)
-  static constexpr int LDK = SK * 8;
-  static constexpr int LDVR = SV * 8;
-  static constexpr int KS = D / 16;             // QK^T k-steps
-  static constexpr int DT = D / 32;             // O^T row tiles (32 dims)
-  static constexpr int NTK = BN / 32;           // S^T key tiles
-  static constexpr int K_INSTR = (BN * SK + 63) / 64;  // wave instructions per K sub-tile
-  static constexpr int V_INSTR = (BN * SV + 63) / 64;
-  static constexpr int K_ELEMS = K_INSTR * 64 * 8;     // uint16 elements
-  static constexpr int V_ELEMS = V_INSTR * 64 * 8;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;
-  static constexpr int WAVES = kThreads / 64;
-  static constexpr int KI_PER_WAVE = (K_INSTR + WAVES - 1) / WAVES;
-  static constexpr int VI_PER_WAVE = (V_INSTR + WAVES - 1) / WAVES;
+// LDS geometry of one K or V sub-tile: BN rows of ROWB bytes (D elements
+// padded to a power of two), 16-byte chunk c of row r stored at chunk
+// c ^ mask(r).  The masks make the 16 rows of a ds_read_b128 quarter-wave hit
+// 16 different 16-byte bank groups, and the 4 rows of a transposing read
+// group 4 different 64-byte bank quarters.
+template <int D, int BN_>
+struct Geom {
+  static constexpr int ROWB = D <= 64 ? 128 : (D <= 128 ? 256 : 512);
+  static constexpr int RC = ROWB / 16;     // chunks per LDS row
+  static constexpr int DG = D / 8;         // chunks holding data
+  static constexpr int BN = BN_;           // keys per sub-tile (32 or 64)
+  static constexpr int TILE = BN * ROWB;   // bytes per K (or V) sub-tile
+  static constexpr int STAGE = 2 * TILE;   // K then V
+  static constexpr int JT = TILE / 1024;   // fill instructions (64 lanes x 16 B) per sub-tile
+  static constexpr int RPI = 64 / RC;      // rows per fill instruction
+  static constexpr int KS = D / 16;        // QK^T k-steps
+  static constexpr int DT = D / 32;        // O^T row tiles (32 dims)
+  static constexpr int NTK = BN / 32;      // S^T key tiles per sub-tile
+  static __device__ __forceinline__ int kmask(int row) {
+    return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
+  }
+  static __device__ __forceinline__ int vmask(int row) {
+    return ROWB >= 256 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+  }
 };
 
 // One K/V sub-tile of the walk: `nkeys` valid rows starting at key `key0`
@@ -137,15 +196,22 @@ struct Step {
   int nkeys;  // valid rows in the sub-tile
 };
 
-template <typename T, int D, bool CORR>
-__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
-  using TL = AttnTile<T, D, CORR>;
+template <typename T, int D, bool CORR, int WAVES, int NST, int BNK>
+__global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
+  using GM = Geom<D, BNK>;
+  static_assert(BNK == 32 || BNK == 64, "sub-tiles of 32 or 64 keys");
+  // asm LDS reads for D <= 128; D = 256 needs more registers than a wave has
+  // and lets the compiler schedule its LDS reads (see lds_read_b128).
+  constexpr bool kAsm = D <= 128;
   using vec8 = typename Elem<T>::vec8;
-  constexpr int BN = TL::BN;
-  // Two LDS stages as separate objects, so stage reads and the asynchronous
-  // fills of the other stage are known not to alias.
-  __shared__ __align__(1024) uint16_t stage0[TL::STAGE];
-  __shared__ __align__(1024) uint16_t stage1[TL::STAGE];
+  constexpr int BN = GM::BN;
+  constexpr int ROWB = GM::ROWB;
+  constexpr int RW = WAVES * 32;          // packed query rows per workgroup
+  constexpr int NIK = GM::JT / WAVES;     // fill instructions per wave per sub-tile
+  constexpr int NI = 2 * NIK;             // ... per stage (K then V)
+  static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
+  static_assert(NST >= 2 && NI * (NST - 2) <= 63, "vmcnt range");
+  __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -165,7 +231,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
 
   // ---- this lane's query row ----
   const int R = a.G * a.tq;
-  const int prow = chunk * kRows + wave * 32 + l32;
+  const int prow = chunk * RW + wave * 32 + l32;
   const bool exists = prow < R;
   int g = 0, pos = 0;
   if (exists) {
@@ -175,7 +241,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const bool row_valid = exists && pos < a.Lq;
   const int qpos_abs = a.offset + pos;
 
-  vec8 qf[TL::KS];
+  vec8 qf[GM::KS];
   {
     const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
     const uint32_t qoff =
@@ -185,7 +251,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
     // factor: for scale < 0 the queries are negated instead (s*c = (-s)*(-c)).
     const uint32_t sign = a.c_scale < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int k = 0; k < TL::KS; ++k) {
+    for (int k = 0; k < GM::KS; ++k) {
       u32x4 v = buf_load16(qr, qoff + (row_valid ? k * 32 : 0));
       v ^= sign;
       qf[k] = as_vec8<T>(v);
@@ -226,14 +292,17 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   const int n_steps = n_sel + n_corr;
 
   // Block ids of the selected list are read 64 at a time into one VGPR (lane
-  // = list entry) and handed out with readlane, so producing a step costs no
-  // memory round trip.  The walk state (list entry, sub-tile) advances
-  // incrementally.
+  // = list entry) and handed out with readlane; the pruned list likewise, 64
+  // entries per VGPR, handed to the fill lanes with ds_bpermute.  The walk
+  // state (list entry, sub-tile) advances incrementally.
   int ids_base = 0;
   int ids_lanes = lane < sel_count ? clampi(ids[lane], 0, Nb - 1) : 0;
-  int cur_li = 0, cur_sub = 0;
-  auto next_step = [&](int it) -> Step {
-    Step s;
+  int pids_lanes = 0;
+  if constexpr (CORR) pids_lanes = lane < pr_count ? clampi(pids[lane], 0, Nb - 1) : 0;
+  int cur_li = 0, cur_sub = 0, walk_it = 0;
+  auto next_step = [&]() -> Step {
+    Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
+    const int it = walk_it++;
     if (it < n_sel) {
       if (cur_li - ids_base >= 64) {
         ids_base += 64;
@@ -241,8 +310,6 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         ids_lanes = li < sel_count ? clampi(ids[li], 0, Nb - 1) : 0;
       }
       const int blk = __builtin_amdgcn_readlane(ids_lanes, cur_li - ids_base);
-      s.corr = 0;
-      s.li = cur_li;
       s.key0 = blk * a.bk + cur_sub * BN;
       int n = min(min(a.bk - cur_sub * BN, BN), a.Lk - s.key0);
       if (s.key0 > abs_last) n = 0;
@@ -251,125 +318,106 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
         cur_sub = 0;
         ++cur_li;
       }
-    } else {
+    } else if (it < n_steps) {
       s.corr = 1;
       s.li = (it - n_sel) * BN;
-      s.key0 = 0;
       s.nkeys = min(pr_count - s.li, BN);
     }
     return s;
   };
 
   // ---- global -> LDS fills (buffer_load_dwordx4 ... lds) ----
-  // Per lane and per wave instruction: the slot's row and its byte offset
-  // within the row pattern (kOOB for pad slots).  Constant over the walk.
+  // Fill instruction i of this wave covers rows [jj*RPI, (jj+1)*RPI) of the K
+  // (i < NIK) or V sub-tile, jj = wave + (i % NIK) * WAVES; lane -> chunk
+  // lane % RC of row jj*RPI + lane / RC, holding data chunk c = that ^ mask.
   const rsrc_t kr = make_rsrc(a.k + h * a.k_hs, a.k_bytes);
   const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
   const rsrc_t pkr = make_rsrc(a.pk + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
   const rsrc_t pvr = make_rsrc(a.pv + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
-  // Per lane and wave instruction, the byte offset of the slot within a
-  // sub-tile of consecutive rows (-1 for pad slots); rows are recomputed only
-  // on the rare partial and correction sub-tiles.
-  int k_pre[TL::KI_PER_WAVE], v_pre[TL::VI_PER_WAVE];
-#pragma unroll
-  for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
-    const int slot = (wave + i * TL::WAVES) * 64 + lane;
-    const int r = slot / TL::SK, c = slot - r * TL::SK;
-    k_pre[i] = (c < TL::DG && r < BN) ? (r * a.k_rs + c * 8) * 2 : -1;
-  }
-#pragma unroll
-  for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
-    const int slot = (wave + i * TL::WAVES) * 64 + lane;
-    const int r = slot / TL::SV, c = slot - r * TL::SV;
-    v_pre[i] = (c < TL::DG && r < BN) ? (r * a.v_rs + c * 8) * 2 : -1;
-  }
-
-  // One K/V fill of `stage` for step s.  `rows_of` gives the slot's row
-  // (BN for pad slots) and its 16-byte chunk.
-  auto slot_of = [&](int j, int per_row, int& row, int& chunk) {
-    const int slot = j * 64 + lane;
-    row = slot / per_row;
-    chunk = slot - row * per_row;
-    if (chunk >= TL::DG || row >= BN) row = BN;
+  auto fill_row = [&](int i, int ln) { return (wave + (i % NIK) * WAVES) * GM::RPI + ln / GM::RC; };
+  auto fill_chunk = [&](int i, int row, int ln) {
+    return (ln % GM::RC) ^ (i < NIK ? GM::kmask(row) : GM::vmask(row));
   };
-  auto fill_step = [&](const Step& s, uint16_t* stage) {
+  // The rare partial and correction fills recompute rows and chunks from an
+  // opaque copy of the lane id, so that their per-lane constants are not
+  // hoisted out of the walk to occupy registers for its whole length.
+  auto opaque_lane = [&]() {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    return ln;
+  };
+  // Byte offset of the lane's chunk relative to the sub-tile's first key
+  // (-1: a pad chunk past D).  Constant over the walk.
+  int pre[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int row = fill_row(i, lane);
+    const int c = fill_chunk(i, row, lane);
+    const int rs = i < NIK ? a.k_rs : a.v_rs;
+    pre[i] = c < GM::DG ? (row * rs + c * 8) * 2 : -1;
+  }
+  const uint32_t smem_lds = lds_addr(smem);
+  auto fill_step = [&](const Step& s, int stage) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
-    if (!s.corr && s.nkeys == BN) {  // full exact sub-tile: offsets only
-      const int kbase = s.key0 * a.k_rs * 2;
-      const int vbase = s.key0 * a.v_rs * 2;
+    // (a lambda returning an LDS pointer would drop the kernel from the host
+    // pass, so the destination is spelled out at each fill)
+    uint8_t* const sp = smem + stage * GM::STAGE;
+    if (!s.corr) {
+      const uint32_t kb = static_cast<uint32_t>(s.key0 * a.k_rs * 2);
+      const uint32_t vb = static_cast<uint32_t>(s.key0 * a.v_rs * 2);
+      if (s.nkeys == BN) {  // full sub-tile
 #pragma unroll
-      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::K_INSTR) {
-          const uint32_t off = k_pre[i] >= 0 ? static_cast<uint32_t>(kbase + k_pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
+        for (int i = 0; i < NI; ++i) {
+          bool ok = true;
+          if constexpr (GM::DG < GM::RC) ok = pre[i] >= 0;
+          const uint32_t off = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              i < NIK ? kr : vr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
+              16, off, 0, 0, 0);
+        }
+      } else {  // partial (end of the keys or of a block) or empty
+        const int ln = opaque_lane();
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+          bool ok = fill_row(i, ln) < s.nkeys;
+          if constexpr (GM::DG < GM::RC) ok = ok && pre[i] >= 0;
+          const uint32_t off = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              i < NIK ? kr : vr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
+              16, off, 0, 0, 0);
         }
       }
+    } else {  // correction: pooled rows of the pruned blocks
+      const int w0 = s.li & 63;  // first entry within pids_lanes
+      const int ln = opaque_lane();
 #pragma unroll
-      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::V_INSTR) {
-          const uint32_t off = v_pre[i] >= 0 ? static_cast<uint32_t>(vbase + v_pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
-                                                   off, 0, 0, 0);
-        }
+      for (int i = 0; i < NI; ++i) {
+        const int row = fill_row(i, ln);
+        const int c = fill_chunk(i, row, ln);
+        const int blk = __builtin_amdgcn_ds_bpermute((w0 + row) * 4, pids_lanes);
+        const bool ok = row < s.nkeys && c < GM::DG;
+        const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            i < NIK ? pkr : pvr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
+            16, off, 0, 0, 0);
       }
-    } else if (!s.corr) {  // partial exact sub-tile (end of the keys / of the block)
-      const int kbase = s.key0 * a.k_rs * 2;
-      const int vbase = s.key0 * a.v_rs * 2;
-#pragma unroll
-      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::K_INSTR) {
-          int row, chunk;
-          slot_of(j, TL::SK, row, chunk);
-          const uint32_t off = row < s.nkeys ? static_cast<uint32_t>(kbase + k_pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(kr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::V_INSTR) {
-          int row, chunk;
-          slot_of(j, TL::SV, row, chunk);
-          const uint32_t off = row < s.nkeys ? static_cast<uint32_t>(vbase + v_pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(vr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
-                                                   off, 0, 0, 0);
-        }
-      }
-    } else {  // correction: gather pooled rows of the pruned blocks
-#pragma unroll
-      for (int i = 0; i < TL::KI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::K_INSTR) {
-          int row, chunk;
-          slot_of(j, TL::SK, row, chunk);
-          const bool ok = row < s.nkeys;
-          const int blk = clampi(pids[ok ? s.li + row : s.li], 0, Nb - 1);
-          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + chunk * 8) * 2) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(stage + j * 512), 16, off, 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < TL::VI_PER_WAVE; ++i) {
-        const int j = wave + i * TL::WAVES;
-        if (j < TL::V_INSTR) {
-          int row, chunk;
-          slot_of(j, TL::SV, row, chunk);
-          const bool ok = row < s.nkeys;
-          const int blk = clampi(pids[ok ? s.li + row : s.li], 0, Nb - 1);
-          const uint32_t off = ok ? static_cast<uint32_t>((blk * D + chunk * 8) * 2) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(pvr, (lds_ptr)(stage + TL::K_ELEMS + j * 512), 16,
-                                                   off, 0, 0, 0);
-        }
+      if (((s.li + BN) & 63) == 0) {  // window used up: fetch the next 64 entries
+        const int li = s.li + BN + lane;
+        pids_lanes = li < pr_count ? clampi(pids[li], 0, Nb - 1) : 0;
       }
     }
   };
-  // Wait for this wave's outstanding fills (vmcnt = 0), then for all waves.
+  // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
+  // of the previous sub-tile, whose last slice is still being multiplied by
+  // V (see the slice pipeline below), is not refilled yet.  The fills of a
+  // stage are complete once at most the LA-1 younger stages' fills (NI
+  // instructions each) are outstanding in this wave, and in every wave after
+  // the barrier.
+  constexpr int LA = NST - 2;
+  static_assert(LA >= 1, "the slice pipeline needs NST >= 3");
   auto fills_done = [&]() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
-    __syncthreads();
+    vm_wait<NI * (LA - 1)>();
+    __builtin_amdgcn_s_barrier();
   };
 
   // ---- accumulators ----
@@ -378,171 +426,254 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   // O / l are rescaled only when some row's max grows past that, so the
   // common case costs no rescale at all.  The result O / l is unchanged.
   constexpr float kRescaleSlack = 8.0f;
-  f32x16 o[TL::DT];
+  f32x16 o[GM::DT];
 #pragma unroll
-  for (int i = 0; i < TL::DT; ++i) o[i] = f32x16{};
+  for (int i = 0; i < GM::DT; ++i) o[i] = f32x16{};
   float m_ref = neg_inf();
   float l_run = 0.f;
 
-  // Per-lane pieces of the transpose-read address of V^T fragments: lane j of
-  // a 16-lane group reads row (j/4) and columns 4*(j%4).. of a 4-key x 16-dim
-  // patch; the transpose hands lane i the 4 keys of dim d0 + i.
+  // LDS read addresses relative to a slice (32 keys of a stage).  K: lane
+  // reads row l32, data chunk 2k + hf -> kbase ^ 32k.  V^T: lane j of a
+  // 16-lane group reads row (j/4) and dims 4*(j%4).. of a 4-key x 16-dim
+  // patch (the transpose hands lane i the 4 keys of dim d0 + i): rows
+  // 16u + 4hf + (lane&15)/4 (+8), dims 32dt + ... -> (vbase ^ 64dt) +
+  // (16u (+8)) * ROWB.  The XOR terms only touch bits below 9, and slice
+  // offsets are multiples of 32 rows, so slice offsets add outside the XOR.
+  const int km = GM::kmask(l32);
+  const uint32_t kbase = smem_lds + l32 * ROWB + ((16 * hf) ^ (16 * km));
   const int tr_row = (lane & 15) >> 2;
-  const int tr_col = (lane & 3) * 4 + ((lane >> 4) & 1) * 16;
+  const int cig = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // chunk within a 64-byte group
+  const int vq = ROWB >= 256 ? tr_row : ((tr_row >> 1) & 1);   // swizzled 64-byte group
+  const uint32_t vbase =
+      smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8;
 
-  // One 32-key slice (key tile kt of the sub-tile): S^T, mask, online softmax
-  // update, P, then O^T += V^T . P^T.  Slicing the 64-key sub-tile keeps only
-  // 16 S and 8 P registers live.
-  auto compute_slice = [&](const Step& s, const uint16_t* stage, int kt) {
-    const uint16_t* ks = stage;
-    const uint16_t* vs = stage + TL::K_ELEMS;
-    f32x16 st = f32x16{};
-#pragma unroll
-    for (int k = 0; k < TL::KS; ++k) {
-      const u32x4 kv = load16(ks + (kt * 32 + l32) * TL::LDK + k * 16 + hf * 8);
-      st = Elem<T>::mfma32(as_vec8<T>(kv), qf[k], st);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // mask (diagonal / partial sub-tiles only) and raw row max
-    const float shift = s.corr ? a.shift : 0.f;
-    const bool need_mask = (s.nkeys < (kt + 1) * 32) || (!s.corr && s.key0 + kt * 32 + 31 > abs_first);
-    if (need_mask) {
-      const int key_lim = s.corr ? BN : qpos_abs - s.key0;  // causal: e <= key_lim
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int e = kt * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
-        st[j] = (e < s.nkeys && e <= key_lim) ? st[j] : neg_inf();
+  // ---- slice pipeline ----
+  // A slice is 32 keys of a sub-tile.  Slices are processed one behind the
+  // other: while the MFMAs of S^T = K . Q^T run for slice n, the VALU works
+  // on the softmax of slice n-1, whose P then multiplies V.  Each wave thus
+  // keeps its matrix pipe busy during its own softmax.
+  struct Slice {
+    int corr;       // pooled correction rows (logit shift, no causal mask)
+    int key0;       // first key (exact slices)
+    int nkeys;      // valid rows from the slice start (may exceed 32)
+    uint32_t off;   // byte offset of the slice within the stage ring
+  };
+  auto make_slice = [&](const Step& s, int stage, int kt) {
+    Slice r;
+    r.corr = s.corr;
+    r.key0 = s.key0 + kt * 32;
+    r.nkeys = s.nkeys - kt * 32;
+    r.off = static_cast<uint32_t>(stage * GM::STAGE + kt * 32 * ROWB);
+    return r;
+  };
+  // Raw S^T of the pending slice, in one of two buffers: the two slices of a
+  // sub-tile alternate between them, so no copy is needed in the common case.
+  f32x16 s_buf[2] = {f32x16{}, f32x16{}};
+  Slice p_pend{0, 0, 0, 0u};
+
+  constexpr int PV_OPS = 2 * GM::DT;  // PV MFMAs per slice: (u, dt)
+  constexpr int PER_BATCH = 4;        // MFMA operands per batch of 8 transposing reads
+  constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
+  auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8]) {
+    constexpr int b = decltype(bc)::value;
+    StaticFor<0, PER_BATCH>::run([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int op = b * PER_BATCH + q;
+      if constexpr (op < PV_OPS) {
+        constexpr int u = op / GM::DT, dt = op % GM::DT;
+        const uint32_t addr = va ^ (64 * dt);
+        r[2 * q] = lds_read_tr<kAsm, u * 16 * ROWB>(addr);
+        r[2 * q + 1] = lds_read_tr<kAsm, (u * 16 + 8) * ROWB>(addr);
+      } else {
+        r[2 * q] = u32x2{0u, 0u};
+        r[2 * q + 1] = u32x2{0u, 0u};
       }
-    }
-    float mx = neg_inf();
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, st[j]), st[j + 1]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
-    const bool upd = __ballot(m_cand > m_ref + kRescaleSlack) != 0ull;
-    float alpha = 1.f;
-    if (upd) {
-      const float m_new = fmaxf(m_ref, m_cand);
-      alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-      m_ref = m_new;
-      l_run *= alpha;
-    }
-    const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
-    vec8 pb[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      u32x4 w;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[u * 8 + 2 * i], c_pos, bias));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[u * 8 + 2 * i + 1], c_pos, bias));
-        w[i] = pack2<T>(p0, p1);
-        l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
-      }
-      pb[u] = as_vec8<T>(w);
-    }
-    if (upd) {
-#pragma unroll
-      for (int dt = 0; dt < TL::DT; ++dt) {
-#pragma unroll
-        for (int j = 0; j < 16; ++j) o[dt][j] *= alpha;
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
-    // transposing LDS reads of the row-major V tile: keys
-    // 32kt + 16u + 4hf + {0..3} and the same + 8, matching the key order of
-    // this lane's P values.  Reads go in batches of 8 (4 MFMA operands): the
-    // second batch is in flight while the first batch's MFMAs run.
-    constexpr int PV_OPS = 2 * TL::DT;  // MFMAs of this slice: (u, dt)
-    constexpr int PER_BATCH = 4;
-    constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
-    // lane part of the address; the (kt, u, dt, +8 keys) parts are immediates
-    const uint32_t vbase = lds_addr(vs) + ((hf * 4 + tr_row) * TL::LDVR + tr_col) * 2;
-    u32x2 rb[2][8];
-    auto issue_batch = [&](auto bc, u32x2 (&r)[8]) {
-      constexpr int b = decltype(bc)::value;
-      StaticFor<0, PER_BATCH>::run([&](auto qc) {
-        constexpr int q = decltype(qc)::value;
-        constexpr int op = b * PER_BATCH + q;
-        if constexpr (op < PV_OPS) {
-          constexpr int u = op / TL::DT, dt = op % TL::DT;
-          constexpr int off = ((u * 16) * TL::LDVR + dt * 32) * 2;
-          r[2 * q] = tr_read<off>(vbase + kt * 32 * TL::LDVR * 2);
-          r[2 * q + 1] = tr_read<off + 8 * TL::LDVR * 2>(vbase + kt * 32 * TL::LDVR * 2);
-        } else {
-          r[2 * q] = u32x2{0u, 0u};
-          r[2 * q + 1] = u32x2{0u, 0u};
-        }
-      });
-    };
-    auto run_batch = [&](auto bc, u32x2 (&r)[8]) {
-      constexpr int b = decltype(bc)::value;
-      StaticFor<0, PER_BATCH>::run([&](auto qc) {
-        constexpr int q = decltype(qc)::value;
-        constexpr int op = b * PER_BATCH + q;
-        if constexpr (op < PV_OPS) {
-          constexpr int u = op / TL::DT, dt = op % TL::DT;
-          const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
-          o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-        }
-      });
-    };
-    issue_batch(std::integral_constant<int, 0>{}, rb[0]);
-    tr_wait(rb[0]);
-    StaticFor<0, BATCHES>::run([&](auto bc) {
-      constexpr int b = decltype(bc)::value;
-      if constexpr (b + 1 < BATCHES) issue_batch(std::integral_constant<int, b + 1>{}, rb[(b + 1) & 1]);
-      run_batch(bc, rb[b & 1]);
-      if constexpr (b + 1 < BATCHES) tr_wait(rb[(b + 1) & 1]);
     });
   };
-  auto compute_step = [&](const Step& s, const uint16_t* stage) {
-#pragma unroll
-    for (int kt = 0; kt < TL::NTK; ++kt) {
-      if (kt * 32 < s.nkeys || kt == 0) compute_slice(s, stage, kt);
-    }
+  auto run_v = [&](auto bc, u32x2 (&r)[8], const vec8 (&pb)[2]) {
+    constexpr int b = decltype(bc)::value;
+    StaticFor<0, PER_BATCH>::run([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int op = b * PER_BATCH + q;
+      if constexpr (op < PV_OPS) {
+        constexpr int u = op / GM::DT, dt = op % GM::DT;
+        const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
+        o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
+      }
+    });
   };
 
-  // ---- pipelined walk over the sub-tiles: the fills of step it+1 run while
-  // step it is multiplied from the other stage; the loop is unrolled by two
-  // so each half uses a fixed stage ----
-  Step cur = next_step(0);
-  if (n_steps > 0) fill_step(cur, stage0);
-  fills_done();
-  for (int it = 0; it < n_steps; it += 2) {
-    {
-      const bool more = it + 1 < n_steps;
-      Step nxt{};
-      if (more) {
-        nxt = next_step(it + 1);
-        fill_step(nxt, stage1);
-      }
-      compute_step(cur, stage0);
-      fills_done();
-      cur = nxt;
-      if (!more) break;
+  // process<HN, HP, B>(nw): S^T of slice nw (if HN) into s_buf[B]
+  // overlapped with softmax and PV of the pending slice (if HP) from
+  // s_buf[1-B]; nw becomes pending.
+  auto process = [&](auto hn_c, auto hp_c, auto b_c, const Slice& nw) {
+    constexpr bool HN = decltype(hn_c)::value;
+    constexpr bool HP = decltype(hp_c)::value;
+    constexpr int B = decltype(b_c)::value;
+    f32x16& s_pend = s_buf[1 - B];
+    constexpr int KW = GM::KS < 4 ? GM::KS : 4;  // K fragment reads in flight
+    constexpr int H1 = GM::KS / 2;               // MFMAs before the rescale branch
+    const uint32_t va = vbase + p_pend.off;
+    const uint32_t ka = kbase + nw.off;
+    u32x2 vb[2][8];
+    u32x4 kf[GM::KS];
+    // V^T batch 0 of the pending slice, then a window of KW K fragments of
+    // the new one; each QK MFMA issues the read KW fragments ahead.  Reads
+    // complete in order, so fragment i is ready once at most the reads issued
+    // after it, min(KW-1, KS-1-i), are outstanding.
+    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
+    if constexpr (HN) {
+      StaticFor<0, KW>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        kf[i] = lds_read_b128<kAsm, 0>(ka ^ (32 * i));
+      });
     }
-    {
-      const bool more = it + 2 < n_steps;
-      Step nxt{};
-      if (more) {
-        nxt = next_step(it + 2);
-        fill_step(nxt, stage0);
+    f32x16& sn = s_buf[B];  // free: the pending slice is in the other buffer
+    if constexpr (HN) sn = f32x16{};
+    auto qk_mfma = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int younger = (GM::KS - 1 - i) < (KW - 1) ? (GM::KS - 1 - i) : (KW - 1);
+      lgkm_wait<kAsm, younger>(kf[i]);
+      sn = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], sn);
+      if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
+    };
+    // pending: mask (diagonal / partial slices only) and row max
+    float m_cand = neg_inf();
+    float shift = 0.f;
+    if constexpr (HP) {
+      shift = p_pend.corr ? a.shift : 0.f;
+      const bool need_mask = p_pend.nkeys < 32 || (!p_pend.corr && p_pend.key0 + 31 > abs_first);
+      if (need_mask) {
+        // Element j holds key e = hf*4 + c_j of the slice, c_j = (j/4)*8 + j%4;
+        // it is kept iff e < nkeys and (correction, or e <= qpos - key0),
+        // i.e. iff c_j <= lim with one per-lane limit, so the 16 tests
+        // compare against immediates.
+        int lim = p_pend.nkeys - 1 - hf * 4;
+        if (!p_pend.corr) lim = min(lim, qpos_abs - p_pend.key0 - hf * 4);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int cj = (j >> 2) * 8 + (j & 3);
+          s_pend[j] = cj <= lim ? s_pend[j] : neg_inf();
+        }
       }
-      compute_step(cur, stage1);
-      fills_done();
-      cur = nxt;
+    }
+    if constexpr (HN) StaticFor<0, H1>::run(qk_mfma);
+    bool upd = false;
+    if constexpr (HP) {
+      float mx = neg_inf();
+#pragma unroll
+      for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, s_pend[j]), s_pend[j + 1]);
+      mx = pair_max(mx);
+      m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
+      upd = __ballot(m_cand > m_ref + kRescaleSlack) != 0ull;
+      if (upd) {
+        const float m_new = fmaxf(m_ref, m_cand);
+        const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        m_ref = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < GM::DT; ++dt) scale_in_place(o[dt], alpha);
+      }
+    }
+    if constexpr (HN) StaticFor<H1, GM::KS>::run(qk_mfma);
+    if constexpr (HP) {
+      const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
+      vec8 pb[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_pend[u * 8 + 2 * i], c_pos, bias));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_pend[u * 8 + 2 * i + 1], c_pos, bias));
+          w[i] = pack2<T>(p0, p1);
+          l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
+        }
+        pb[u] = as_vec8<T>(w);
+      }
+      // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
+      // transposing reads: keys 16u + 4hf + {0..3} and the same + 8, matching
+      // the key order of this lane's P values.
+      lgkm_wait<kAsm, 0>(vb[0]);
+      StaticFor<0, BATCHES>::run([&](auto bc) {
+        constexpr int b = decltype(bc)::value;
+        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
+        run_v(bc, vb[b & 1], pb);
+        if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
+      });
+    }
+    if constexpr (HN) p_pend = nw;
+  };
+
+  // ---- pipelined walk: sub-tile `it` is multiplied from stage it % NST
+  // while the fills of the next LA sub-tiles are in flight.  Fills past the
+  // end load an empty sub-tile so every iteration issues the same number of
+  // fills. ----
+  Step pend[LA];
+#pragma unroll
+  for (int p = 0; p < LA; ++p) {
+    pend[p] = next_step();
+    fill_step(pend[p], p);
+  }
+  using True = std::integral_constant<bool, true>;
+  using False = std::integral_constant<bool, false>;
+  int cstage = 0;
+  // One sub-tile.  The pending slice enters in s_buf[P] and leaves in
+  // s_buf[P] (two slices) or s_buf[1-P] (one slice per sub-tile).
+  auto do_step = [&](auto first_c, auto p_c) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    constexpr int P = decltype(p_c)::value;
+    using NewB = std::integral_constant<int, 1 - P>;
+    using PendB = std::integral_constant<int, P>;
+    fills_done();  // sub-tile it is in LDS; sub-tile it-2's stage is free
+    const Step cur = pend[0];
+#pragma unroll
+    for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
+    pend[LA - 1] = next_step();
+    const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
+    fill_step(pend[LA - 1], fstage);
+    const Slice s0 = make_slice(cur, cstage, 0);
+    if constexpr (FIRST) process(True{}, False{}, NewB{}, s0);
+    else process(True{}, True{}, NewB{}, s0);
+    if constexpr (GM::NTK > 1) {
+      if (cur.nkeys > 32) process(True{}, True{}, PendB{}, make_slice(cur, cstage, 1));
+      else s_buf[P] = s_buf[1 - P];
+    }
+    cstage = cstage == NST - 1 ? 0 : cstage + 1;
+  };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  if (n_steps > 0) {
+    do_step(True{}, P0{});  // the first sub-tile has no pending slice
+    if constexpr (GM::NTK > 1) {
+      for (int it = 1; it < n_steps; ++it) do_step(False{}, P0{});
+      process(False{}, True{}, P1{}, p_pend);  // pending in s_buf[0]
+    } else {
+      // one slice per sub-tile: the pending buffer alternates, so two
+      // sub-tiles per iteration
+      int it = 1;
+      for (; it + 1 < n_steps; it += 2) {
+        do_step(False{}, P1{});
+        do_step(False{}, P0{});
+      }
+      if (it < n_steps) {
+        do_step(False{}, P1{});
+        process(False{}, True{}, P1{}, p_pend);  // pending in s_buf[0]
+      } else {
+        process(False{}, True{}, P0{}, p_pend);  // pending in s_buf[1]
+      }
     }
   }
+  // No fill may land in LDS after the workgroup ends.
+  vm_wait<0>();
 
   // ---- normalise and store ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float l_tot = pair_sum(l_run);
   if (!exists || pos >= a.out_rows) return;
   const float inv = (row_valid && l_tot > 0.f) ? 1.f / l_tot : 0.f;
   uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g) * a.o_hs + pos * a.o_rs;
 #pragma unroll
-  for (int dt = 0; dt < TL::DT; ++dt) {
+  for (int dt = 0; dt < GM::DT; ++dt) {
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       const int d0 = dt * 32 + jg * 8 + hf * 4;
@@ -554,22 +685,38 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void sparse_attn_kern
   }
 }
 
-template <typename T, int D, bool CORR>
-int launch_attn(const AttnArgs& a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR>;
+template <typename T, int D, bool CORR, int WAVES, int NST, int BNK>
+int launch_attn(AttnArgs a, hipStream_t stream) {
+  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, BNK>;
+  a.nchunk = (a.G * a.tq + WAVES * 32 - 1) / (WAVES * 32);
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
   if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(WAVES * 64), 0, stream, a);
   return check_launch("sparse_attention");
+}
+
+// Workgroup shape.  D <= 128: 8 waves (256 rows) over 64-key sub-tiles in a
+// 4-stage ring (128 KiB, one workgroup per CU) when the packed rows of a tile
+// come in multiples of 256; else 4 waves (128 rows) over 32-key sub-tiles in
+// a 4-stage ring (64 KiB, two workgroups per CU).  D = 256: 4 waves, 32-key
+// sub-tiles, 128 KiB.
+template <typename T, int D, bool CORR>
+int launch_shape(const AttnArgs& a, hipStream_t s) {
+  if constexpr (D <= 128) {
+    if ((static_cast<int64_t>(a.G) * a.tq) % 256 == 0) return launch_attn<T, D, CORR, 8, 4, 64>(a, s);
+    return launch_attn<T, D, CORR, 4, 4, 32>(a, s);
+  } else {
+    return launch_attn<T, D, CORR, 4, 4, 32>(a, s);
+  }
 }
 
 template <typename T>
 int dispatch_attn(int64_t D, bool corr, const AttnArgs& a, hipStream_t s) {
   switch (D) {
-    case 64: return corr ? launch_attn<T, 64, true>(a, s) : launch_attn<T, 64, false>(a, s);
-    case 96: return corr ? launch_attn<T, 96, true>(a, s) : launch_attn<T, 96, false>(a, s);
-    case 128: return corr ? launch_attn<T, 128, true>(a, s) : launch_attn<T, 128, false>(a, s);
-    case 256: return corr ? launch_attn<T, 256, true>(a, s) : launch_attn<T, 256, false>(a, s);
+    case 64: return corr ? launch_shape<T, 64, true>(a, s) : launch_shape<T, 64, false>(a, s);
+    case 96: return corr ? launch_shape<T, 96, true>(a, s) : launch_shape<T, 96, false>(a, s);
+    case 128: return corr ? launch_shape<T, 128, true>(a, s) : launch_shape<T, 128, false>(a, s);
+    case 256: return corr ? launch_shape<T, 256, true>(a, s) : launch_shape<T, 256, false>(a, s);
     default:
       return fail(FPV2_ERR_UNSUPPORTED, "head dimension must be one of (64, 96, 128, 256)");
   }
@@ -626,7 +773,7 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
     return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: a head group spans more than 2 GiB");
   if (p->q_row_stride < D || p->k_row_stride < D || p->v_row_stride < D || p->o_row_stride < D)
     return fail(FPV2_ERR_ARGUMENT, "sparse_attention: row strides must be >= head_dim");
-  if (p->kv_heads * Nt * ((G * p->tile_q + kRows - 1) / kRows) > 0x7fffffffLL ||
+  if (p->kv_heads * Nt * ((G * p->tile_q + 127) / 128) > 0x7fffffffLL ||
       p->num_blocks * p->block_k > 0x7fffffffLL || G * p->tile_q > 0x7fffffffLL ||
       p->padded_query_length > 0x7fffffffLL)
     return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: sizes exceed 32-bit indexing");
@@ -651,7 +798,6 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
   a.offset = static_cast<int>(p->offset);
   a.bk = static_cast<int>(p->block_k);
   a.tq = static_cast<int>(p->tile_q);
-  a.nchunk = static_cast<int>((G * p->tile_q + kRows - 1) / kRows);
   a.c_scale = static_cast<float>(p->scale * 1.4426950408889634);
   a.shift = static_cast<float>(__builtin_log2(static_cast<double>(p->block_k)));
   a.q_hs = p->q_head_stride;
