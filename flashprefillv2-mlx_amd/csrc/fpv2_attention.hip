@@ -448,10 +448,14 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
       smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8;
 
   // ---- slice pipeline ----
-  // A slice is 32 keys of a sub-tile.  Slices are processed one behind the
-  // other: while the MFMAs of S^T = K . Q^T run for slice n, the VALU works
-  // on the softmax of slice n-1, whose P then multiplies V.  Each wave thus
-  // keeps its matrix pipe busy during its own softmax.
+  // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
+  // stages, one process() call apart, so that every stage pairs MFMA work
+  // with VALU work of another slice:
+  //   A: S^T = K . Q^T of slice n       ||  exp2 / pack / row sum of slice n-1
+  //   B: O^T += V^T . P^T of slice n-1  ||  mask and row max of slice n
+  //   C: (rare) rescale of O and l when slice n raises the reference max.
+  // A wave keeps its matrix pipe busy during its own softmax; the order of
+  // issue within A and B is fixed with scheduling-group barriers.
   struct Slice {
     int corr;       // pooled correction rows (logit shift, no causal mask)
     int key0;       // first key (exact slices)
@@ -466,8 +470,8 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
     r.off = static_cast<uint32_t>(stage * GM::STAGE + kt * 32 * ROWB);
     return r;
   };
-  // Raw S^T of the pending slice, in one of two buffers: the two slices of a
-  // sub-tile alternate between them, so no copy is needed in the common case.
+  // S^T of the slice between stages A and B of the pipeline (masked, its max
+  // folded into m_ref), in one of two buffers that alternate between slices.
   f32x16 s_buf[2] = {f32x16{}, f32x16{}};
   Slice p_pend{0, 0, 0, 0u};
 
@@ -490,83 +494,128 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
       }
     });
   };
-  auto run_v = [&](auto bc, u32x2 (&r)[8], const vec8 (&pb)[2]) {
-    constexpr int b = decltype(bc)::value;
-    StaticFor<0, PER_BATCH>::run([&](auto qc) {
-      constexpr int q = decltype(qc)::value;
-      constexpr int op = b * PER_BATCH + q;
-      if constexpr (op < PV_OPS) {
-        constexpr int u = op / GM::DT, dt = op % GM::DT;
-        const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
-        o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-      }
-    });
+  // process<HN, HP, B>(nw): stage A and B for the new slice nw (if HN, into
+  // s_buf[B]) and the pending slice (if HP, in s_buf[1-B]); nw becomes
+  // pending.
+  auto needs_mask = [&](const Slice& nw) {
+    return nw.nkeys < 32 || (!nw.corr && nw.key0 + 31 > abs_first);
   };
-
-  // process<HN, HP, B>(nw): S^T of slice nw (if HN) into s_buf[B]
-  // overlapped with softmax and PV of the pending slice (if HP) from
-  // s_buf[1-B]; nw becomes pending.
-  auto process = [&](auto hn_c, auto hp_c, auto b_c, const Slice& nw) {
+  auto process_m = [&](auto hn_c, auto hp_c, auto b_c, auto mask_c, const Slice& nw) {
     constexpr bool HN = decltype(hn_c)::value;
     constexpr bool HP = decltype(hp_c)::value;
     constexpr int B = decltype(b_c)::value;
-    f32x16& s_pend = s_buf[1 - B];
+    constexpr bool MASK = decltype(mask_c)::value;
+    f32x16& s_new = s_buf[B];
+    f32x16& s_old = s_buf[1 - B];
     constexpr int KW = GM::KS < 4 ? GM::KS : 4;  // K fragment reads in flight
-    constexpr int H1 = GM::KS / 2;               // MFMAs before the rescale branch
     const uint32_t va = vbase + p_pend.off;
     const uint32_t ka = kbase + nw.off;
     u32x2 vb[2][8];
     u32x4 kf[GM::KS];
+    vec8 pb[2];
+
+    // ---- stage A ----
     // V^T batch 0 of the pending slice, then a window of KW K fragments of
     // the new one; each QK MFMA issues the read KW fragments ahead.  Reads
     // complete in order, so fragment i is ready once at most the reads issued
-    // after it, min(KW-1, KS-1-i), are outstanding.
+    // after it, min(KW-1, KS-1-i), are outstanding.  The exp section of the
+    // pending slice is spread over the QK MFMAs in source order; an empty asm
+    // that consumes each piece keeps the compiler from regrouping them.
     if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
     if constexpr (HN) {
       StaticFor<0, KW>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         kf[i] = lds_read_b128<kAsm, 0>(ka ^ (32 * i));
       });
+      s_new = f32x16{};
     }
-    f32x16& sn = s_buf[B];  // free: the pending slice is in the other buffer
-    if constexpr (HN) sn = f32x16{};
-    auto qk_mfma = [&](auto ic) {
-      constexpr int i = decltype(ic)::value;
-      constexpr int younger = (GM::KS - 1 - i) < (KW - 1) ? (GM::KS - 1 - i) : (KW - 1);
-      lgkm_wait<kAsm, younger>(kf[i]);
-      sn = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], sn);
-      if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
-    };
-    // pending: mask (diagonal / partial slices only) and row max
-    float m_cand = neg_inf();
-    float shift = 0.f;
+    float bias = 0.f;
     if constexpr (HP) {
-      shift = p_pend.corr ? a.shift : 0.f;
-      const bool need_mask = p_pend.nkeys < 32 || (!p_pend.corr && p_pend.key0 + 31 > abs_first);
-      if (need_mask) {
-        // Element j holds key e = hf*4 + c_j of the slice, c_j = (j/4)*8 + j%4;
-        // it is kept iff e < nkeys and (correction, or e <= qpos - key0),
-        // i.e. iff c_j <= lim with one per-lane limit, so the 16 tests
-        // compare against immediates.
-        int lim = p_pend.nkeys - 1 - hf * 4;
-        if (!p_pend.corr) lim = min(lim, qpos_abs - p_pend.key0 - hf * 4);
+      const float shift = p_pend.corr ? a.shift : 0.f;
+      bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
+    }
+    u32x4 w[2];
+    // P for the pair of keys (2pi, 2pi+1) of the pending slice
+    auto exp_pair = [&](auto pc) {
+      constexpr int pi = decltype(pc)::value;
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_old[2 * pi], c_pos, bias));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_old[2 * pi + 1], c_pos, bias));
+      const uint32_t word = pack2<T>(p0, p1);
+      l_run = add_pair<T>(word, l_run);  // row sum of the rounded P used below
+      w[pi / 4][pi % 4] = word;
+      asm volatile("" ::"v"(word));
+    };
+    if constexpr (HN) {
+      StaticFor<0, GM::KS>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int younger = (GM::KS - 1 - i) < (KW - 1) ? (GM::KS - 1 - i) : (KW - 1);
+        lgkm_wait<kAsm, younger>(kf[i]);
+        s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
+        if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
+        if constexpr (HP) StaticFor<i * 8 / GM::KS, (i + 1) * 8 / GM::KS>::run(exp_pair);
+      });
+    } else if constexpr (HP) {
+      StaticFor<0, 8>::run(exp_pair);
+    }
+    if constexpr (HP) {
+      pb[0] = as_vec8<T>(w[0]);
+      pb[1] = as_vec8<T>(w[1]);
+    }
+
+    // mask of the new slice (diagonal / partial slices only)
+    if constexpr (HN && MASK) {
+      // Element j holds key e = hf*4 + c_j of the slice, c_j = (j/4)*8 + j%4;
+      // it is kept iff e < nkeys and (correction, or e <= qpos - key0), i.e.
+      // iff c_j <= lim with one per-lane limit, so the 16 tests compare
+      // against immediates.
+      int lim = nw.nkeys - 1 - hf * 4;
+      if (!nw.corr) lim = min(lim, qpos_abs - nw.key0 - hf * 4);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int cj = (j >> 2) * 8 + (j & 3);
-          s_pend[j] = cj <= lim ? s_pend[j] : neg_inf();
-        }
+      for (int j = 0; j < 16; ++j) {
+        const int cj = (j >> 2) * 8 + (j & 3);
+        s_new[j] = cj <= lim ? s_new[j] : neg_inf();
       }
     }
-    if constexpr (HN) StaticFor<0, H1>::run(qk_mfma);
-    bool upd = false;
+
+    // ---- stage B ----
+    // PV MFMAs of the pending slice with the row max of the new one spread
+    // over them.
+    float mx = neg_inf();
+    auto max_step = [&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      mx = fmaxf(fmaxf(mx, s_new[2 * j]), s_new[2 * j + 1]);
+      asm volatile("" : "+v"(mx));
+    };
     if constexpr (HP) {
-      float mx = neg_inf();
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) mx = fmaxf(fmaxf(mx, s_pend[j]), s_pend[j + 1]);
+      lgkm_wait<kAsm, 0>(vb[0]);
+      StaticFor<0, BATCHES>::run([&](auto bc) {
+        constexpr int b = decltype(bc)::value;
+        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
+        StaticFor<0, PER_BATCH>::run([&](auto qc) {
+          constexpr int q = decltype(qc)::value;
+          constexpr int op = b * PER_BATCH + q;
+          if constexpr (op < PV_OPS) {
+            constexpr int u = op / GM::DT, dt = op % GM::DT;
+            const u32x2(&r)[8] = vb[b & 1];
+            const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
+            o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
+            if constexpr (HN) StaticFor<op * 8 / PV_OPS, (op + 1) * 8 / PV_OPS>::run(max_step);
+          }
+        });
+        if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
+      });
+    } else if constexpr (HN) {
+      StaticFor<0, 8>::run(max_step);
+    }
+    float m_cand = neg_inf();
+    if constexpr (HN) {
       mx = pair_max(mx);
-      m_cand = fmaf(mx, c_pos, shift);  // -inf stays -inf (c_pos > 0)
-      upd = __ballot(m_cand > m_ref + kRescaleSlack) != 0ull;
-      if (upd) {
+      m_cand = fmaf(mx, c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
+    }
+
+    // ---- stage C: reference max of the new slice ----
+    if constexpr (HN) {
+      if (__ballot(m_cand > m_ref + kRescaleSlack) != 0ull) {
         const float m_new = fmaxf(m_ref, m_cand);
         const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
         m_ref = m_new;
@@ -574,35 +623,18 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
 #pragma unroll
         for (int dt = 0; dt < GM::DT; ++dt) scale_in_place(o[dt], alpha);
       }
+      p_pend = nw;
     }
-    if constexpr (HN) StaticFor<H1, GM::KS>::run(qk_mfma);
-    if constexpr (HP) {
-      const float bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
-      vec8 pb[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        u32x4 w;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_pend[u * 8 + 2 * i], c_pos, bias));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_pend[u * 8 + 2 * i + 1], c_pos, bias));
-          w[i] = pack2<T>(p0, p1);
-          l_run = add_pair<T>(w[i], l_run);  // row sum of the rounded P used below
-        }
-        pb[u] = as_vec8<T>(w);
-      }
-      // O^T += V^T . P^T.  The A operand (8 keys x 32 dims) comes from two
-      // transposing reads: keys 16u + 4hf + {0..3} and the same + 8, matching
-      // the key order of this lane's P values.
-      lgkm_wait<kAsm, 0>(vb[0]);
-      StaticFor<0, BATCHES>::run([&](auto bc) {
-        constexpr int b = decltype(bc)::value;
-        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
-        run_v(bc, vb[b & 1], pb);
-        if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
-      });
+  };
+  // The mask decision is taken before the call so that stages A and B stay
+  // free of branches.
+  auto process = [&](auto hn_c, auto hp_c, auto b_c, const Slice& nw) {
+    if constexpr (decltype(hn_c)::value) {
+      if (needs_mask(nw)) process_m(hn_c, hp_c, b_c, std::true_type{}, nw);
+      else process_m(hn_c, hp_c, b_c, std::false_type{}, nw);
+    } else {
+      process_m(hn_c, hp_c, b_c, std::false_type{}, nw);
     }
-    if constexpr (HN) p_pend = nw;
   };
 
   // ---- pipelined walk: sub-tile `it` is multiplied from stage it % NST
