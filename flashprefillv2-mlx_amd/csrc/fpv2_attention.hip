@@ -476,6 +476,15 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   Slice p_pend{0, 0, 0, 0u};
 
   constexpr int PV_OPS = 2 * GM::DT;  // PV MFMAs per slice: (u, dt)
+  // issue-order tuning of the slice pipeline (see process_m)
+#ifndef FPV2_EXP_LEAD
+#define FPV2_EXP_LEAD 0
+#endif
+#ifndef FPV2_MAX_DELAY
+#define FPV2_MAX_DELAY 0
+#endif
+  constexpr int kExpLead = FPV2_EXP_LEAD;   // exp pairs issued before the first QK MFMA
+  constexpr int kMaxDelay = FPV2_MAX_DELAY; // PV MFMAs issued before the first row-max step
   constexpr int PER_BATCH = 4;        // MFMA operands per batch of 8 transposing reads
   constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
   auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8]) {
@@ -546,13 +555,18 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
       asm volatile("" ::"v"(word));
     };
     if constexpr (HN) {
+      // kExpLead pairs first, while the first K fragments are in flight,
+      // then the rest spread over the QK MFMAs.
+      constexpr int E0 = HP ? kExpLead : 0;
+      if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
       StaticFor<0, GM::KS>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         constexpr int younger = (GM::KS - 1 - i) < (KW - 1) ? (GM::KS - 1 - i) : (KW - 1);
         lgkm_wait<kAsm, younger>(kf[i]);
         s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
         if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
-        if constexpr (HP) StaticFor<i * 8 / GM::KS, (i + 1) * 8 / GM::KS>::run(exp_pair);
+        if constexpr (HP)
+          StaticFor<E0 + i * (8 - E0) / GM::KS, E0 + (i + 1) * (8 - E0) / GM::KS>::run(exp_pair);
       });
     } else if constexpr (HP) {
       StaticFor<0, 8>::run(exp_pair);
@@ -599,7 +613,10 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
             const u32x2(&r)[8] = vb[b & 1];
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
             o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-            if constexpr (HN) StaticFor<op * 8 / PV_OPS, (op + 1) * 8 / PV_OPS>::run(max_step);
+            // the row max starts kMaxDelay MFMAs in, when S^T has landed
+            constexpr int DM = kMaxDelay < PV_OPS ? kMaxDelay : PV_OPS - 1;
+            if constexpr (HN && op >= DM)
+              StaticFor<(op - DM) * 8 / (PV_OPS - DM), (op - DM + 1) * 8 / (PV_OPS - DM)>::run(max_step);
           }
         });
         if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
