@@ -153,6 +153,7 @@ struct AttnArgs {
   float c_scale;  // scale * log2(e)
   float shift;    // log2(block_k)
   int64_t q_hs, k_hs, v_hs, o_hs, o_rs;
+  int64_t pooled_hs;  // elements between KV heads of pk / pv
   int q_rs, k_rs, v_rs;
   uint32_t q_bytes, k_bytes, v_bytes, pooled_bytes;  // descriptor ranges
 };
@@ -332,8 +333,8 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   // lane % RC of row jj*RPI + lane / RC, holding data chunk c = that ^ mask.
   const rsrc_t kr = make_rsrc(a.k + h * a.k_hs, a.k_bytes);
   const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
-  const rsrc_t pkr = make_rsrc(a.pk + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
-  const rsrc_t pvr = make_rsrc(a.pv + static_cast<int64_t>(h) * Nb * D, a.pooled_bytes);
+  const rsrc_t pkr = make_rsrc(a.pk + h * a.pooled_hs, a.pooled_bytes);
+  const rsrc_t pvr = make_rsrc(a.pv + h * a.pooled_hs, a.pooled_bytes);
   auto fill_row = [&](int i, int ln) { return (wave + (i % NIK) * WAVES) * GM::RPI + ln / GM::RC; };
   auto fill_chunk = [&](int i, int row, int ln) {
     return (ln % GM::RC) ^ (i < NIK ? GM::kmask(row) : GM::vmask(row));
@@ -807,6 +808,10 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
                               p->o_head_stride, p->o_row_stride};
   for (int i = 0; i < 8; ++i)
     if (strides[i] % 8) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: strides must be multiples of 8 elements");
+  if (p->pooled_head_stride < p->num_blocks * p->head_dim)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention: pooled_head_stride must be >= num_blocks*head_dim");
+  if (p->pooled_head_stride % 8)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: strides must be multiples of 8 elements");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(pooled_k) ||
       !aligned16(pooled_v) || reinterpret_cast<uintptr_t>(out) % 8)
     return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: tensors must be 16-byte aligned");
@@ -854,6 +859,7 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
   a.v_hs = p->v_head_stride;
   a.o_hs = p->o_head_stride;
   a.o_rs = p->o_row_stride;
+  a.pooled_hs = p->pooled_head_stride;
   a.q_rs = static_cast<int>(p->q_row_stride);
   a.k_rs = static_cast<int>(p->k_row_stride);
   a.v_rs = static_cast<int>(p->v_row_stride);

@@ -55,6 +55,7 @@ struct PoolArgs {
   int64_t block_size;
   int64_t batch_stride;
   int64_t row_stride;
+  int64_t out_batch_stride;  // elements between batches of dst
 };
 
 // 16-bit element types: 16-byte vector loads.
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool16_kernel(PoolArgs a) {
   __syncthreads();
   // Combine row groups: thread (col, i) sums column element col*V+i.
   const int total = cols * V;
-  uint16_t* dst = static_cast<uint16_t*>(a.dst[which]) + (n * a.num_blocks + b) * a.head_dim;
+  uint16_t* dst = static_cast<uint16_t*>(a.dst[which]) + n * a.out_batch_stride + b * a.head_dim;
   for (int e = tid; e < total; e += kPoolThreads) {
     const int c = e / V;
     const int i = e - c * V;
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_generic_kernel(PoolArgs a) 
     if (tid < cols && c0 + tid < a.head_dim) {
       double t = 0.0;
       for (int g = 0; g < groups; ++g) t += red[g * cols + tid];
-      store_elem<T>(a.dst[which], (n * a.num_blocks + b) * a.head_dim + c0 + tid,
+      store_elem<T>(a.dst[which], n * a.out_batch_stride + b * a.head_dim + c0 + tid,
                     t / static_cast<double>(a.block_size));
     }
     __syncthreads();
@@ -175,6 +176,8 @@ int launch_pool(const PoolArgs& a, int tensors, int dtype, hipStream_t stream) {
     return fail(FPV2_ERR_ARGUMENT, "pool: valid_rows must lie in [0, num_blocks*block_size]");
   for (int i = 0; i < tensors; ++i)
     if (!a.src[i] || !a.dst[i]) return fail(FPV2_ERR_ARGUMENT, "pool: null pointer");
+  if (a.batch > 1 && a.out_batch_stride < a.num_blocks * a.head_dim)
+    return fail(FPV2_ERR_ARGUMENT, "pool: out_batch_stride must be >= num_blocks*head_dim");
   const int64_t items = a.batch * a.num_blocks;
   if (items > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "pool: too many blocks");
   dim3 grid(static_cast<unsigned>(items), tensors);
@@ -211,7 +214,7 @@ int launch_pool(const PoolArgs& a, int tensors, int dtype, hipStream_t stream) {
 extern "C" int fpv2_pool_blocks(const void* x, void* out, int dtype, int64_t batch,
                                 int64_t valid_rows, int64_t num_blocks, int64_t head_dim,
                                 int64_t block_size, int64_t batch_stride, int64_t row_stride,
-                                void* stream) {
+                                int64_t out_batch_stride, void* stream) {
   fpv2::PoolArgs a{};
   a.src[0] = x;
   a.dst[0] = out;
@@ -222,13 +225,14 @@ extern "C" int fpv2_pool_blocks(const void* x, void* out, int dtype, int64_t bat
   a.block_size = block_size;
   a.batch_stride = batch_stride;
   a.row_stride = row_stride;
+  a.out_batch_stride = out_batch_stride;
   return fpv2::launch_pool(a, 1, dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fpv2_pool_kv(const void* k, const void* v, void* pooled_k, void* pooled_v,
                             int dtype, int64_t kv_heads, int64_t valid_rows, int64_t num_blocks,
                             int64_t head_dim, int64_t block_size, int64_t head_stride,
-                            int64_t row_stride, void* stream) {
+                            int64_t row_stride, int64_t pooled_head_stride, void* stream) {
   fpv2::PoolArgs a{};
   a.src[0] = k;
   a.src[1] = v;
@@ -241,5 +245,6 @@ extern "C" int fpv2_pool_kv(const void* k, const void* v, void* pooled_k, void* 
   a.block_size = block_size;
   a.batch_stride = head_stride;
   a.row_stride = row_stride;
+  a.out_batch_stride = pooled_head_stride;
   return fpv2::launch_pool(a, 2, dtype, static_cast<hipStream_t>(stream));
 }

@@ -26,6 +26,7 @@ struct SelectArgs {
   int64_t G, Hkv, Nt, Nb, Lq_pad, Lq, Lk, offset, bk, tq, sink, window, last_n;
   float scale, alpha;
   int64_t q_hs, q_rs;
+  int64_t pk_hs;  // elements between KV heads of pk
   uint8_t* sel_out;
   float* scores;
   int32_t* ids;
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
   const int hf = lane >> 5;
   const int64_t R = a.G * a.tq;
   const int64_t n_comp = a.scores ? a.Nb : ti.nfv;
-  const uint16_t* pk = static_cast<const uint16_t*>(a.pk) + ti.h * a.Nb * D;
+  const uint16_t* pk = static_cast<const uint16_t*>(a.pk) + ti.h * a.pk_hs;
   const uint16_t* qbase = static_cast<const uint16_t*>(a.q);
 
   for (int64_t b = tid; b < n_comp; b += kThreads) {
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(kThreads) void select_generic_kernel(SelectArgs a, 
       for (int r = 0; r < kGenericRows && rc + r < R; ++r) {
         const int64_t pr = rc + r;
         float dot = 0.f;
-        for (int d = 0; d < D; ++d) dot = fmaf(qs[r * D + d], ld<T>(a.pk, (ti.h * a.Nb + b) * D + d), dot);
+        for (int d = 0; d < D; ++d) dot = fmaf(qs[r * D + d], ld<T>(a.pk, ti.h * a.pk_hs + b * D + d), dot);
         const float s = dot * a.scale;
         const int64_t g = pr / a.tq;
         const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
@@ -496,6 +497,8 @@ extern "C" int fpv2_score_select(const void* q, const void* pooled_k, int dtype,
   if (any_list && !all_list) return fail(FPV2_ERR_ARGUMENT, "score_select: give all four list outputs or none");
   if (any_list && (p->key_length <= 0 || p->key_length > p->num_blocks * p->block_k))
     return fail(FPV2_ERR_ARGUMENT, "key_length is inconsistent with selected blocks");
+  if (p->pooled_head_stride < p->num_blocks * p->head_dim)
+    return fail(FPV2_ERR_ARGUMENT, "score_select: pooled_head_stride must be >= num_blocks*head_dim");
   SelectArgs a{};
   a.q = q;
   a.pk = pooled_k;
@@ -516,6 +519,7 @@ extern "C" int fpv2_score_select(const void* q, const void* pooled_k, int dtype,
   a.alpha = p->alpha;
   a.q_hs = p->q_head_stride;
   a.q_rs = p->q_row_stride;
+  a.pk_hs = p->pooled_head_stride;
   a.sel_out = selected;
   a.scores = scores;
   a.ids = selected_ids;
@@ -527,7 +531,7 @@ extern "C" int fpv2_score_select(const void* q, const void* pooled_k, int dtype,
   dim3 grid(static_cast<unsigned>(wgs));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t D = p->head_dim;
-  const bool vec_ok = D % 8 == 0 && a.q_rs % 8 == 0 && a.q_hs % 8 == 0 &&
+  const bool vec_ok = D % 8 == 0 && a.q_rs % 8 == 0 && a.q_hs % 8 == 0 && a.pk_hs % 8 == 0 &&
                       reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(pooled_k) % 16 == 0;
   bool done = false;

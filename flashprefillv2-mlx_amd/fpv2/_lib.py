@@ -16,7 +16,7 @@ import torch
 LIB_NAME = "libfpv2_hip.so"
 # The in-tree build; FPV2_LIBRARY may point at another build of the same ABI.
 LIB_PATH = Path(os.environ.get("FPV2_LIBRARY") or Path(__file__).resolve().parent / LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FPV2_OK = 0
 FPV2_ERR_ARGUMENT = -1
@@ -60,6 +60,7 @@ class SelectParams(ctypes.Structure):
         ("alpha", ctypes.c_float),
         ("q_head_stride", ctypes.c_int64),
         ("q_row_stride", ctypes.c_int64),
+        ("pooled_head_stride", ctypes.c_int64),
     ]
 
 
@@ -88,6 +89,7 @@ class AttnParams(ctypes.Structure):
         ("v_row_stride", ctypes.c_int64),
         ("o_head_stride", ctypes.c_int64),
         ("o_row_stride", ctypes.c_int64),
+        ("pooled_head_stride", ctypes.c_int64),
     ]
 
 
@@ -101,9 +103,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fpv2_last_error.restype = ctypes.c_char_p
     lib.fpv2_last_error.argtypes = []
     lib.fpv2_pool_blocks.restype = ctypes.c_int
-    lib.fpv2_pool_blocks.argtypes = [vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, vp]
+    lib.fpv2_pool_blocks.argtypes = [vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
     lib.fpv2_pool_kv.restype = ctypes.c_int
-    lib.fpv2_pool_kv.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, vp]
+    lib.fpv2_pool_kv.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp]
     lib.fpv2_score_select.restype = ctypes.c_int
     lib.fpv2_score_select.argtypes = [vp, vp, i32, ctypes.POINTER(SelectParams), vp, vp,
                                       vp, vp, vp, vp, vp]

@@ -234,6 +234,17 @@ def sparse_attention(
     return out
 
 
+def _pooled_ready(pooled_k: torch.Tensor, pooled_v: torch.Tensor):
+    """Pooled K/V as the kernel reads them: blocks and D contiguous, one head
+    stride shared by both (a pooled cache with spare capacity is used in
+    place)."""
+    def ok(p):
+        return p.stride(-1) == 1 and p.stride(-2) == p.shape[-1] and p.stride(0) % 8 == 0
+    if not (ok(pooled_k) and ok(pooled_v) and pooled_k.stride(0) == pooled_v.stride(0)):
+        pooled_k, pooled_v = pooled_k.contiguous(), pooled_v.contiguous()
+    return pooled_k, pooled_v
+
+
 def _launch_attention(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts,
                       pruned_ids, pruned_counts, out, *, device, scale, config, offset,
                       query_length, key_length, num_blocks, padded_query_length,
@@ -246,7 +257,7 @@ def _launch_attention(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts
     """
     lib = _lib.load()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    pooled_k, pooled_v = pooled_k.contiguous(), pooled_v.contiguous()
+    pooled_k, pooled_v = _pooled_ready(pooled_k, pooled_v)
     ids, counts = selected_ids.contiguous(), selected_counts.contiguous()
     pids, pcounts = pruned_ids.contiguous(), pruned_counts.contiguous()
     params = _lib.AttnParams(
@@ -258,7 +269,8 @@ def _launch_attention(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts
         q_head_stride=q.stride(0), q_row_stride=q.stride(1),
         k_head_stride=k.stride(0), k_row_stride=k.stride(1),
         v_head_stride=v.stride(0), v_row_stride=v.stride(1),
-        o_head_stride=out.stride(0), o_row_stride=out.stride(1))
+        o_head_stride=out.stride(0), o_row_stride=out.stride(1),
+        pooled_head_stride=pooled_k.stride(0))
     with torch.cuda.device(device):
         status = lib.fpv2_sparse_attention(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), pooled_k.data_ptr(),

@@ -23,7 +23,7 @@ the ``[1, Hq, Lq, D]`` output directly.  ``disable`` restores the original.
 
 from __future__ import annotations
 
-from dataclasses import replace
+from dataclasses import dataclass, replace
 from typing import Any
 
 import torch
@@ -121,11 +121,26 @@ def fpv2_sdpa(
     return _fpv2_sdpa(q, k, v, scale=scale, config=config)
 
 
-def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
-    """``fpv2_sdpa`` body.  ``marks(name)`` (optional) is called on the host
-    between the launches ("select", "attention", "done") so a caller can
-    record stream events around each kernel; ``keep`` (optional dict)
-    receives the pooled tensors and block lists of the call."""
+@dataclass(frozen=True)
+class _Geometry:
+    """Sizes of one hook call (``patch.py:116-136`` without the padding copies)."""
+
+    config: FPV2Config
+    query_heads: int
+    kv_heads: int
+    head_dim: int
+    query_length: int
+    key_length: int
+    offset: int
+    padded_query_length: int
+    num_tiles: int
+    num_blocks: int
+
+
+def _geometry(q, k, v, config: FPV2Config) -> _Geometry:
+    """The reference hook's validation (``patch.py:102-124``) and the block
+    grid: Q padded to a ``tile_q`` multiple, keys to ``ceil(max(Lk, off +
+    Lq_pad) / block_k)`` blocks, as index arithmetic only."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, and v must have shape [batch, heads, sequence, dim]")
     if q.shape[0] != 1 or k.shape[0] != 1 or v.shape[0] != 1:
@@ -145,47 +160,60 @@ def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
     if q.dtype not in (torch.float16, torch.bfloat16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, and v must share float16 or bfloat16 dtype")
     offset = key_length - query_length
-
-    query_heads, kv_heads, head_dim = q.shape[1], k.shape[1], q.shape[-1]
     padded_query_length = -(-query_length // config.tile_q) * config.tile_q
     required_key_length = max(key_length, offset + padded_query_length)
     padded_key_length = -(-required_key_length // config.block_k) * config.block_k
-    num_tiles = padded_query_length // config.tile_q
     num_blocks = padded_key_length // config.block_k
     if num_blocks > _lib.MAX_BLOCKS:
         raise ValueError(f"key length needs {num_blocks} blocks; at most {_lib.MAX_BLOCKS}")
+    return _Geometry(config=config, query_heads=q.shape[1], kv_heads=k.shape[1],
+                     head_dim=q.shape[-1], query_length=query_length, key_length=key_length,
+                     offset=offset, padded_query_length=padded_query_length,
+                     num_tiles=padded_query_length // config.tile_q, num_blocks=num_blocks)
 
-    device = _lib.require_device(q, k, v)
+
+def _pool_into(lib, k3, v3, pooled_k, pooled_v, *, dtype, valid_rows, num_blocks,
+               block_k, stream) -> None:
+    """Pool ``num_blocks`` blocks of ``k3``/``v3`` (``[Hkv, rows, D]`` views;
+    rows >= ``valid_rows`` count as zeros) into ``pooled_k``/``pooled_v``
+    (``[Hkv, >=num_blocks, D]`` views, any head stride)."""
+    kv_heads, _, head_dim = k3.shape
+    if k3.stride() == v3.stride() and pooled_k.stride() == pooled_v.stride():
+        status = lib.fpv2_pool_kv(
+            k3.data_ptr(), v3.data_ptr(), pooled_k.data_ptr(), pooled_v.data_ptr(),
+            dtype, kv_heads, valid_rows, num_blocks, head_dim, block_k,
+            k3.stride(0), k3.stride(1), pooled_k.stride(0), stream)
+        _lib.check(status, "pool_kv")
+        return
+    for src, dst in ((k3, pooled_k), (v3, pooled_v)):
+        status = lib.fpv2_pool_blocks(
+            src.data_ptr(), dst.data_ptr(), dtype, kv_heads, valid_rows, num_blocks,
+            head_dim, block_k, src.stride(0), src.stride(1), dst.stride(0), stream)
+        _lib.check(status, "pool_blocks")
+
+
+def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out=None,
+                   marks=None, keep=None):
+    """Selection and block-sparse attention of one hook call, given the
+    pooled K/V (``[Hkv, >=Nb, D]`` views sharing one head stride).  Writes
+    ``out`` (``[Hq, Lq, D]``, allocated when None) and returns it."""
+    config = geo.config
+    device = q3.device
     lib = _lib.load()
-    q3, k3, v3 = _kernel_ready(q[0]), _kernel_ready(k[0]), _kernel_ready(v[0])
     stream = _lib.stream_ptr(device)
-    dtype = _lib.dtype_code(q.dtype)
-
-    pooled_k = torch.empty((kv_heads, num_blocks, head_dim), dtype=q.dtype, device=device)
-    pooled_v = torch.empty_like(pooled_k)
+    dtype = _lib.dtype_code(q3.dtype)
+    kv_heads, num_tiles, num_blocks = geo.kv_heads, geo.num_tiles, geo.num_blocks
     ids = torch.empty((kv_heads, num_tiles, num_blocks), dtype=torch.int32, device=device)
     pruned_ids = torch.empty_like(ids)
     counts = torch.empty((kv_heads, num_tiles), dtype=torch.int32, device=device)
     pruned_counts = torch.empty_like(counts)
     with torch.cuda.device(device):
-        if marks is not None:
-            marks("pool")
-        if k3.stride() == v3.stride():
-            status = lib.fpv2_pool_kv(
-                k3.data_ptr(), v3.data_ptr(), pooled_k.data_ptr(), pooled_v.data_ptr(),
-                dtype, kv_heads, key_length, num_blocks, head_dim, config.block_k,
-                k3.stride(0), k3.stride(1), stream)
-            _lib.check(status, "pool_kv")
-        else:
-            for src, dst in ((k3, pooled_k), (v3, pooled_v)):
-                status = lib.fpv2_pool_blocks(
-                    src.data_ptr(), dst.data_ptr(), dtype, kv_heads, key_length,
-                    num_blocks, head_dim, config.block_k, src.stride(0), src.stride(1),
-                    stream)
-                _lib.check(status, "pool_blocks")
         params = _select_params(q3, num_blocks, kv_heads=kv_heads, scale=scale,
-                                config=config, offset=offset, query_length=query_length,
-                                padded_length=padded_query_length, key_length=key_length)
+                                config=config, offset=geo.offset,
+                                query_length=geo.query_length,
+                                padded_length=geo.padded_query_length,
+                                key_length=geo.key_length,
+                                pooled_head_stride=pooled_k.stride(0))
         if marks is not None:
             marks("select")
         status = lib.fpv2_score_select(
@@ -195,20 +223,47 @@ def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
     if _collect_stats:
         global _visible_blocks
         _selected_counts.append(counts)
-        _visible_blocks += _causal_block_count(kv_heads, query_length, offset, config)
-    out = torch.empty((1, query_heads, query_length, head_dim), dtype=q.dtype, device=device)
+        _visible_blocks += _causal_block_count(kv_heads, geo.query_length, geo.offset, config)
+    if out is None:
+        out = torch.empty((geo.query_heads, geo.query_length, geo.head_dim),
+                          dtype=q3.dtype, device=device)
     if marks is not None:
         marks("attention")
     _launch_attention(
-        q3, k3, v3, pooled_k, pooled_v, ids, counts, pruned_ids, pruned_counts, out[0],
-        device=device, scale=scale, config=config, offset=offset,
-        query_length=query_length, key_length=key_length, num_blocks=num_blocks,
-        padded_query_length=padded_query_length, out_rows=query_length)
+        q3, k3, v3, pooled_k, pooled_v, ids, counts, pruned_ids, pruned_counts, out,
+        device=device, scale=scale, config=config, offset=geo.offset,
+        query_length=geo.query_length, key_length=geo.key_length, num_blocks=num_blocks,
+        padded_query_length=geo.padded_query_length, out_rows=geo.query_length)
     if marks is not None:
         marks("done")
     if keep is not None:
-        keep.update(config=config, offset=offset, pooled_k=pooled_k, pooled_v=pooled_v,
+        keep.update(config=config, offset=geo.offset, pooled_k=pooled_k, pooled_v=pooled_v,
                     lists=(ids, counts, pruned_ids, pruned_counts))
+    return out
+
+
+def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
+    """``fpv2_sdpa`` body.  ``marks(name)`` (optional) is called on the host
+    between the launches ("pool", "select", "attention", "done") so a caller
+    can record stream events around each kernel; ``keep`` (optional dict)
+    receives the pooled tensors and block lists of the call."""
+    geo = _geometry(q, k, v, config)
+    device = _lib.require_device(q, k, v)
+    lib = _lib.load()
+    q3, k3, v3 = _kernel_ready(q[0]), _kernel_ready(k[0]), _kernel_ready(v[0])
+    pooled_k = torch.empty((geo.kv_heads, geo.num_blocks, geo.head_dim), dtype=q.dtype,
+                           device=device)
+    pooled_v = torch.empty_like(pooled_k)
+    with torch.cuda.device(device):
+        if marks is not None:
+            marks("pool")
+        _pool_into(lib, k3, v3, pooled_k, pooled_v, dtype=_lib.dtype_code(q.dtype),
+                   valid_rows=geo.key_length, num_blocks=geo.num_blocks,
+                   block_k=geo.config.block_k, stream=_lib.stream_ptr(device))
+    out = torch.empty((1, geo.query_heads, geo.query_length, geo.head_dim), dtype=q.dtype,
+                      device=device)
+    _select_attend(q3, k3, v3, pooled_k, pooled_v, geo, scale=scale, out=out[0],
+                   marks=marks, keep=keep)
     return out
 
 

@@ -100,7 +100,7 @@ def pool_blocks(x: torch.Tensor, block_size: int = 128) -> torch.Tensor:
         status = lib.fpv2_pool_blocks(
             flat.data_ptr(), out.data_ptr(), _lib.dtype_code(x.dtype), flat.shape[0],
             length, num_blocks, head_dim, block_size, flat.stride(0), flat.stride(1),
-            _lib.stream_ptr(device))
+            num_blocks * head_dim, _lib.stream_ptr(device))
     _lib.check(status, "pool_blocks")
     return out
 
@@ -134,7 +134,8 @@ def _validate_inputs(
 
 def _select_params(q: torch.Tensor, num_blocks: int, *, kv_heads: int, scale: float,
                    config: FPV2Config, offset: int, query_length: int,
-                   padded_length: int, key_length: int) -> _lib.SelectParams:
+                   padded_length: int, key_length: int,
+                   pooled_head_stride: int | None = None) -> _lib.SelectParams:
     return _lib.SelectParams(
         query_heads=q.shape[0], kv_heads=kv_heads, head_dim=q.shape[-1],
         padded_query_length=padded_length, query_length=query_length,
@@ -142,7 +143,9 @@ def _select_params(q: torch.Tensor, num_blocks: int, *, kv_heads: int, scale: fl
         block_k=config.block_k, tile_q=config.tile_q,
         sink_tokens=config.sink_tokens, window_tokens=config.window_tokens,
         last_n_blocks=config.last_n_blocks, scale=float(scale), alpha=float(config.alpha),
-        q_head_stride=q.stride(0), q_row_stride=q.stride(1))
+        q_head_stride=q.stride(0), q_row_stride=q.stride(1),
+        pooled_head_stride=(num_blocks * q.shape[-1] if pooled_head_stride is None
+                            else pooled_head_stride))
 
 
 def _operands(q: torch.Tensor, pooled_k: torch.Tensor):

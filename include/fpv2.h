@@ -12,7 +12,9 @@
  * Layouts (row-major, element strides; the last dimension is contiguous):
  *   q        [Hq,  Lq, D]  query heads, head h uses KV head h / (Hq / Hkv)
  *   k, v     [Hkv, Lk, D]
- *   pooled   [Hkv, Nb, D]  contiguous, Nb = ceil(rows / block_k)
+ *   pooled   [Hkv, Nb, D]  rows and D contiguous, any head stride (a pooled
+ *                          cache with spare block capacity is used in place),
+ *                          Nb = ceil(rows / block_k)
  *   lists    [Hkv, Nt, Nb] int32 contiguous, Nt = padded_query_length / tile_q
  *   counts   [Hkv, Nt]     int32 contiguous
  *   selected [Hkv, Nt, Nb] uint8 (0/1) contiguous
@@ -28,7 +30,7 @@
 extern "C" {
 #endif
 
-#define FPV2_ABI_VERSION 1
+#define FPV2_ABI_VERSION 2
 
 typedef enum fpv2_status {
   FPV2_OK = 0,
@@ -67,6 +69,8 @@ typedef struct fpv2_select_params {
   float alpha;
   int64_t q_head_stride; /* elements between query heads               */
   int64_t q_row_stride;  /* elements between query positions           */
+  int64_t pooled_head_stride; /* elements between KV heads of pooled_k,
+                                 >= num_blocks * head_dim                 */
 } fpv2_select_params;
 
 /* Attention parameters.  Mirrors the argument list of sparse_attention,
@@ -92,6 +96,8 @@ typedef struct fpv2_attn_params {
   int64_t k_head_stride, k_row_stride;
   int64_t v_head_stride, v_row_stride;
   int64_t o_head_stride, o_row_stride;
+  int64_t pooled_head_stride; /* elements between KV heads of pooled_k and
+                                 pooled_v, >= num_blocks * head_dim        */
 } fpv2_attn_params;
 
 /* ABI version (FPV2_ABI_VERSION) and the last error of this thread. */
@@ -100,25 +106,29 @@ const char* fpv2_last_error(void);
 
 /*
  * Mean-pool `rows` of x[batch, rows, D] into out[batch, num_blocks, D]
- * (contiguous), block b averaging rows [b*block_size, (b+1)*block_size);
- * rows >= valid_rows count as zeros.  The mean is computed in float64 and
- * rounded once to the output dtype (= input dtype).
+ * (rows and D contiguous, out_batch_stride elements between batches), block
+ * b averaging rows [b*block_size, (b+1)*block_size); rows >= valid_rows count
+ * as zeros.  The mean is computed in float64 and rounded once to the output
+ * dtype (= input dtype).  Pooling a range of blocks of a longer sequence is
+ * the same call with x and out advanced to the first block.
  * Replaces pool_blocks, fpv2/selection.py:68-80.
  */
 int fpv2_pool_blocks(const void* x, void* out, int dtype, int64_t batch,
                      int64_t valid_rows, int64_t num_blocks, int64_t head_dim,
                      int64_t block_size, int64_t batch_stride,
-                     int64_t row_stride, void* stream);
+                     int64_t row_stride, int64_t out_batch_stride, void* stream);
 
 /*
  * Pool K and V of one attention layer in a single launch (the two
  * pool_blocks calls of fpv2/patch.py:137-138).  k and v share geometry and
- * strides; pooled_k / pooled_v are contiguous [kv_heads, num_blocks, D].
+ * strides; pooled_k / pooled_v are [kv_heads, num_blocks, D] with
+ * pooled_head_stride elements between heads.
  */
 int fpv2_pool_kv(const void* k, const void* v, void* pooled_k, void* pooled_v,
                  int dtype, int64_t kv_heads, int64_t valid_rows,
                  int64_t num_blocks, int64_t head_dim, int64_t block_size,
-                 int64_t head_stride, int64_t row_stride, void* stream);
+                 int64_t head_stride, int64_t row_stride,
+                 int64_t pooled_head_stride, void* stream);
 
 /*
  * Pooled-QK scoring and block selection, one workgroup per

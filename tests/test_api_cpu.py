@@ -233,19 +233,55 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert loaded.fpv2_abi_version() == _lib.ABI_VERSION
 
 
-def test_abi_struct_layouts_match_header():
-    # every int64 field is 8-byte aligned; the float pair / int32+double padding
-    assert ctypes.sizeof(_lib.SelectParams) == 8 * 15 + 8
-    assert ctypes.sizeof(_lib.AttnParams) == 8 * 11 + 8 + 8 + 8 * 8
+def test_abi_struct_layouts_match_header(tmp_path):
+    """ctypes mirrors of fpv2_select_params / fpv2_attn_params match the C
+    header field by field (offsets and sizes, as compiled by gcc)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    include = Path(__file__).resolve().parents[1] / "include"
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "fpv2.h"', "int main(void) {"]
+    for cname, cls in (("fpv2_select_params", _lib.SelectParams),
+                       ("fpv2_attn_params", _lib.AttnParams)):
+        lines.append(f'  printf("{cls.__name__} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cls.__name__} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-I", str(include), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    for line in out.splitlines():
+        cls_name, field, value = line.split()
+        cls = getattr(_lib, cls_name)
+        expected = ctypes.sizeof(cls) if field == "size" else getattr(cls, field).offset
+        assert int(value) == expected, line
 
 
 def test_library_rejects_bad_arguments_without_a_gpu():
     if not _lib.LIB_PATH.exists():
         pytest.skip("libfpv2_hip.so not built")
     lib = _lib.load()
-    status = lib.fpv2_pool_blocks(None, None, _lib.BF16, 1, 8, 1, 8, 8, 64, 8, None)
+    status = lib.fpv2_pool_blocks(None, None, _lib.BF16, 1, 8, 1, 8, 8, 64, 8, 64, None)
     assert status == _lib.FPV2_ERR_ARGUMENT
     assert b"null" in lib.fpv2_last_error()
     params = _lib.AttnParams(query_heads=3, kv_heads=2)
     status = lib.fpv2_sparse_attention(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, _lib.BF16, params, None)
     assert status == _lib.FPV2_ERR_ARGUMENT
+
+
+def test_chunked_prefill_validation_without_a_gpu():
+    from fpv2 import ChunkedPrefill
+    with pytest.raises(ValueError, match="divisible"):
+        ChunkedPrefill(8, 3, 128, 64, device="cpu")
+    with pytest.raises(ValueError, match="head dimension"):
+        ChunkedPrefill(8, 2, 100, 64, device="cpu")
+    with pytest.raises(ValueError, match="capacity"):
+        ChunkedPrefill(8, 2, 128, 0, device="cpu")
+    with pytest.raises(ValueError, match="total_tokens"):
+        ChunkedPrefill(8, 2, 128, 64, total_tokens=0, device="cpu")
+    with pytest.raises(RuntimeError, match="ROCm"):
+        ChunkedPrefill(8, 2, 128, 64, device="cpu")

@@ -68,7 +68,7 @@ def test_pool_kv_partial_last_block_counts_zeros(cuda):
     pv = torch.empty_like(pk)
     status = lib.fpv2_pool_kv(kd.data_ptr(), vd.data_ptr(), pk.data_ptr(), pv.data_ptr(),
                               _lib.BF16, 4, 300, 3, 128, 128, kd.stride(0), kd.stride(1),
-                              _lib.stream_ptr(cuda))
+                              pk.stride(0), _lib.stream_ptr(cuda))
     _lib.check(status, "pool_kv")
     pad = np.zeros((4, 384, 128), np.float32)
     pad[:, :300] = to_np(k)
@@ -218,7 +218,7 @@ def _hook_select(q, k, config, *, total_tokens=None):
     pk = torch.empty((hkv, nb, d), dtype=q.dtype, device=dev)
     status = lib.fpv2_pool_blocks(k.data_ptr(), pk.data_ptr(), _lib.dtype_code(q.dtype), hkv,
                                   lk, nb, d, cfg.block_k, k.stride(0), k.stride(1),
-                                  _lib.stream_ptr(dev))
+                                  pk.stride(0), _lib.stream_ptr(dev))
     _lib.check(status, "pool")
     from fpv2.selection import _select_params
     ids = torch.empty((hkv, nt, nb), dtype=torch.int32, device=dev)
