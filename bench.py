@@ -225,6 +225,90 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
     }
 
 
+def run_chunked(torch, total: int, chunk: int, alpha: float):
+    """one layer's chunked prefill of ``total`` tokens in
+    ``chunk``-token query chunks against a growing bf16 KV cache, dense tail
+    only on the last chunk (``total_tokens`` known).  Times the incremental
+    pooled cache (``fpv2.ChunkedPrefill``) and, beside it, the reference
+    hook's per-chunk re-pooling of the whole prefix (``fpv2_sdpa``)."""
+    from fpv2 import ChunkedPrefill, FPV2Config
+    from fpv2.patch import _fpv2_sdpa
+    from fpv2.synthetic import baseline_qkv
+
+    dev = torch.device("cuda:0")
+    log(f"chunked {total} in {chunk}-token chunks: generating inputs")
+    q, k, v = baseline_qkv(total, planted=3.0, heavy_fraction=heavy_fraction(total), seed=0,
+                           device=dev)
+    config = FPV2Config(alpha=alpha, sink_tokens=BLOCK, mean_correction=True)
+    scale = D ** -0.5
+    stream = torch.cuda.current_stream(dev)
+
+    def one_pass(incremental: bool, keeps=None):
+        cp = ChunkedPrefill(HQ, HKV, D, total, config=config, total_tokens=total, device=dev)
+        events = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s0 in range(0, total, chunk):
+            s1 = min(s0 + chunk, total)
+            ev = {}
+
+            def marks(name, ev=ev):
+                e = torch.cuda.Event(enable_timing=True)
+                e.record(stream)
+                ev[name] = e
+            keep = {} if keeps is not None else None
+            cp.append(k[:, s0:s1], v[:, s0:s1])
+            if incremental:
+                cp.attend(q[:, s0:s1], scale=scale, marks=marks, keep=keep)
+            else:
+                _fpv2_sdpa(q[None, :, s0:s1], k[None, :, :s1], v[None, :, :s1], scale=scale,
+                           config=cp.request_config(), marks=marks, keep=keep)
+            events.append(ev)
+            if keeps is not None:
+                keeps.append((keep, s1 - s0))
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        stage = {"pool": 0.0, "select": 0.0, "attention": 0.0}
+        for ev in events:
+            stage["pool"] += ev["pool"].elapsed_time(ev["select"])
+            stage["select"] += ev["select"].elapsed_time(ev["attention"])
+            stage["attention"] += ev["attention"].elapsed_time(ev["done"])
+        return wall, stage, cp.pooled_rows
+
+    one_pass(True)  # warm-up
+    keeps = []
+    wall, stage, pooled_rows = one_pass(True, keeps)
+    one_pass(False)
+    wall_re, stage_re, _ = one_pass(False)
+    f_ret = f_dense = 0
+    for keep, lq in keeps:
+        f, _ = retained_flops(keep, lq, torch)
+        f_ret += f
+        off = keep["offset"]
+        f_dense += 4 * D * HQ * (lq * off + lq * (lq + 1) // 2)
+    res = {
+        "total_tokens": total,
+        "chunk": chunk,
+        "chunks": -(-total // chunk),
+        "alpha": alpha,
+        "ms_total": wall,
+        "tok_per_s": total / (wall * 1e-3),
+        "stage_ms": stage,
+        "pooled_rows": pooled_rows,
+        "repool_ms_total": wall_re,
+        "repool_stage_ms": stage_re,
+        "repool_rows": sum(min(s0 + chunk, total) for s0 in range(0, total, chunk)),
+        "retained_flops": f_ret,
+        "dense_flops": f_dense,
+        "density": f_ret / f_dense,
+        "retained_tflops_attention": f_ret / (stage["attention"] * 1e-3) / 1e12,
+    }
+    log(f"chunked {total}/{chunk}: {wall:.1f} ms ({res['tok_per_s']:.0f} tok/s), stages "
+        f"{json.dumps({k_: round(v_, 3) for k_, v_ in stage.items()})}; hook-style re-pooling "
+        f"{wall_re:.1f} ms, pool {stage_re['pool']:.3f} ms")
+    return res
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -239,6 +323,9 @@ def main(argv=None) -> int:
     ap.add_argument("--extended", action="store_true",
                     help="also run the 32k no-corr ablation, the 128k alpha sweep and the "
                          "high-contrast variant")
+    ap.add_argument("--chunked", action="store_true",
+                    help="also run BASELINE config 4 (65536 tokens in 2048-token chunks over a "
+                         "growing KV cache); included in --extended")
     ap.add_argument("--profile", action="store_true",
                     help="primary config only, no CPU baseline (for rocprofv3 runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -284,6 +371,8 @@ def main(argv=None) -> int:
         c, _ = run_config(torch, args.seq, args.alpha, args.steps, args.warmup,
                           planted=3.0 * math.sqrt(D))
         extra["contrast_variant"] = c
+    if (args.extended or args.chunked) and not args.profile:
+        extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
     cpu = None
     if not args.profile and args.cpu_budget > 0:
         cpu = cpu_baseline(torch, data, args.seq, args.alpha, args.cpu_budget)
