@@ -326,6 +326,10 @@ def main(argv=None) -> int:
     ap.add_argument("--chunked", action="store_true",
                     help="also run BASELINE config 4 (65536 tokens in 2048-token chunks over a "
                          "growing KV cache); included in --extended")
+    ap.add_argument("--e2e", action="store_true",
+                    help="also run BASELINE config 5 (random-init Qwen3-4B-architecture "
+                         "prefill of 65536 tokens in 2048-token chunks, FPV2 vs dense); "
+                         "included in --extended")
     ap.add_argument("--profile", action="store_true",
                     help="primary config only, no CPU baseline (for rocprofv3 runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -373,6 +377,12 @@ def main(argv=None) -> int:
         extra["contrast_variant"] = c
     if (args.extended or args.chunked) and not args.profile:
         extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
+    if (args.extended or args.e2e) and not args.profile:
+        from fpv2.prefill_harness import QWEN3_4B, measure
+        log("e2e: random-init Qwen3-4B-architecture prefill, 65536 tokens, 2048-token chunks")
+        e2e = measure(QWEN3_4B, tokens=65536, chunk=2048, alpha=args.alpha, device="cuda:0")
+        log(f"e2e: {json.dumps(e2e)}")
+        extra["e2e_qwen3_4b_64k"] = e2e
     cpu = None
     if not args.profile and args.cpu_budget > 0:
         cpu = cpu_baseline(torch, data, args.seq, args.alpha, args.cpu_budget)

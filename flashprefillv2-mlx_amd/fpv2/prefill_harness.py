@@ -1,0 +1,203 @@
+"""End-to-end chunked prefill of a random-init Qwen3-architecture decoder.
+
+Measurement harness for the reference's end-to-end prefill comparison
+(``README.md:30-46``, driven by ``fpv2/generate.py:49-130`` through mlx-lm):
+the same decoder architecture with random weights (there is no network for
+checkpoints), a prompt of uniform-random token ids fed in fixed-size chunks,
+and attention either through FPV2 (``ChunkedPrefill`` per layer: incremental
+pooling, selection, block-sparse attention) or dense.  Dense runs the same
+kernels with every visible block selected (``alpha = 0``), which is exact
+causal attention; it keeps the comparison on one attention implementation and
+stays off torch's batched bf16 attention paths.
+
+Architecture (Qwen3 as mlx-lm implements it): RMSNorm before attention and
+MLP, per-head RMSNorm of Q and K, rotary embedding (rotate-half, theta 1e6),
+grouped-query attention, SwiGLU MLP, final RMSNorm, tied LM head.  Linear
+layers are plain 2-D GEMMs (``torch.nn.functional.linear``); norms and RoPE
+compute in float32 and store bf16.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from fpv2.chunked import ChunkedPrefill
+from fpv2.selection import FPV2Config
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    layers: int = 36
+    hidden: int = 2560
+    query_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 9728
+    vocab: int = 151936
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-6
+
+
+QWEN3_4B = DecoderShape()
+
+
+def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+
+def rope_tables(shape: DecoderShape, positions: torch.Tensor):
+    """cos/sin ``[L, D]`` of rotate-half RoPE for integer positions."""
+    half = shape.head_dim // 2
+    inv = shape.rope_theta ** (-torch.arange(half, device=positions.device, dtype=torch.float64) / half)
+    ang = positions.to(torch.float64)[:, None] * inv[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().float(), ang.sin().float()
+
+
+def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x ``[L, H, D]`` (float32) rotated by position."""
+    half = x.shape[-1] // 2
+    rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+    return x * cos[:, None, :] + rot * sin[:, None, :]
+
+
+class RandomDecoder:
+    """Random-init decoder weights (normal, std 0.02; norms at 1)."""
+
+    def __init__(self, shape: DecoderShape, *, device, dtype=torch.bfloat16, seed: int = 0):
+        self.shape, self.device, self.dtype = shape, torch.device(device), dtype
+        gen = torch.Generator(device=self.device).manual_seed(seed)
+
+        def w(*dims):
+            return (torch.randn(dims, generator=gen, device=self.device, dtype=torch.float32)
+                    * 0.02).to(dtype)
+
+        s = shape
+        qd, kd = s.query_heads * s.head_dim, s.kv_heads * s.head_dim
+        self.embed = w(s.vocab, s.hidden)
+        self.layers = []
+        for _ in range(s.layers):
+            self.layers.append({
+                "attn_norm": torch.ones(s.hidden, device=self.device, dtype=dtype),
+                "qkv": w(qd + 2 * kd, s.hidden),  # fused q/k/v projection
+                "q_norm": torch.ones(s.head_dim, device=self.device, dtype=dtype),
+                "k_norm": torch.ones(s.head_dim, device=self.device, dtype=dtype),
+                "o": w(s.hidden, qd),
+                "mlp_norm": torch.ones(s.hidden, device=self.device, dtype=dtype),
+                "gate_up": w(2 * s.intermediate, s.hidden),
+                "down": w(s.hidden, s.intermediate),
+            })
+        self.final_norm = torch.ones(s.hidden, device=self.device, dtype=dtype)
+
+    def parameters(self) -> int:
+        n = self.embed.numel() + self.final_norm.numel()
+        for layer in self.layers:
+            n += sum(t.numel() for t in layer.values())
+        return n
+
+
+class ChunkedPrefillRunner:
+    """Chunked prefill of one prompt through a ``RandomDecoder``.
+
+    ``attention``: ``"fpv2"`` (FPV2 with ``config``) or ``"dense"`` (same
+    kernels, every visible block).  ``min_tokens`` is the hook's gate: calls
+    with fewer keys attend densely in both modes.
+    """
+
+    def __init__(self, model: RandomDecoder, capacity: int, *, attention: str = "fpv2",
+                 config: FPV2Config | None = None, min_tokens: int = 4_096):
+        if attention not in ("fpv2", "dense"):
+            raise ValueError("attention must be 'fpv2' or 'dense'")
+        s = model.shape
+        base = config if config is not None else FPV2Config()
+        if attention == "dense":
+            base = FPV2Config(alpha=0.0, block_k=base.block_k, tile_q=base.tile_q,
+                              sink_tokens=base.sink_tokens, window_tokens=base.window_tokens,
+                              last_n_blocks=base.last_n_blocks,
+                              mean_correction=base.mean_correction)
+        self.model, self.capacity, self.attention = model, capacity, attention
+        self.caches = [ChunkedPrefill(s.query_heads, s.kv_heads, s.head_dim, capacity,
+                                      dtype=model.dtype, device=model.device, config=base,
+                                      total_tokens=capacity, min_tokens=min_tokens)
+                       for _ in range(s.layers)]
+
+    def reset(self) -> None:
+        for cache in self.caches:
+            cache.reset()
+
+    def _layer(self, li: int, x: torch.Tensor, cos, sin) -> torch.Tensor:
+        s, p = self.model.shape, self.model.layers[li]
+        L = x.shape[0]
+        qd, kd = s.query_heads * s.head_dim, s.kv_heads * s.head_dim
+        h = _rms_norm(x, p["attn_norm"], s.rms_eps)
+        qkv = F.linear(h, p["qkv"])
+        q = qkv[:, :qd].view(L, s.query_heads, s.head_dim)
+        k = qkv[:, qd:qd + kd].view(L, s.kv_heads, s.head_dim)
+        v = qkv[:, qd + kd:].view(L, s.kv_heads, s.head_dim)
+        q = _apply_rope(_rms_norm(q, p["q_norm"], s.rms_eps).float(), cos, sin).to(x.dtype)
+        k = _apply_rope(_rms_norm(k, p["k_norm"], s.rms_eps).float(), cos, sin).to(x.dtype)
+        # [L, H, D] -> [H, L, D] views; the kernels read any head/row stride
+        out = self.caches[li].step(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1),
+                                   scale=s.head_dim ** -0.5)
+        attn = out[0].transpose(0, 1).reshape(L, qd)
+        x = x + F.linear(attn, p["o"])
+        h = _rms_norm(x, p["mlp_norm"], s.rms_eps)
+        gu = F.linear(h, p["gate_up"])
+        gate, up = gu[:, :s.intermediate], gu[:, s.intermediate:]
+        return x + F.linear(F.silu(gate) * up, p["down"])
+
+    def prefill(self, tokens: torch.Tensor, chunk: int) -> torch.Tensor:
+        """Run the prompt in ``chunk``-token pieces; returns the logits of the
+        last position (float32 ``[vocab]``)."""
+        m = self.model
+        n = tokens.numel()
+        if n > self.capacity:
+            raise ValueError("prompt longer than the KV cache capacity")
+        x = None
+        for start in range(0, n, chunk):
+            end = min(start + chunk, n)
+            pos = torch.arange(start, end, device=m.device)
+            cos, sin = rope_tables(m.shape, pos)
+            x = m.embed[tokens[start:end]]
+            for li in range(m.shape.layers):
+                x = self._layer(li, x, cos, sin)
+        last = _rms_norm(x[-1:], m.final_norm, m.shape.rms_eps)
+        return F.linear(last, m.embed).float()[0]
+
+
+def measure(shape: DecoderShape, *, tokens: int, chunk: int, alpha: float, device,
+            seed: int = 0, modes=("fpv2", "dense"), reps: int = 1) -> dict:
+    """Prefill tok/s and time to first token (prefill + first logits) per mode."""
+    model = RandomDecoder(shape, device=device, seed=seed)
+    gen = torch.Generator(device=model.device).manual_seed(seed + 1)
+    prompt = torch.randint(0, shape.vocab, (tokens,), generator=gen, device=model.device)
+    res = {"parameters": model.parameters(), "tokens": tokens, "chunk": chunk, "alpha": alpha}
+    logits = {}
+    for mode in modes:
+        runner = ChunkedPrefillRunner(model, tokens, attention=mode,
+                                      config=FPV2Config(alpha=alpha, sink_tokens=128))
+        runner.prefill(prompt[:min(tokens, 2 * chunk)], chunk)  # warm-up
+        best = math.inf
+        for _ in range(reps):
+            runner.reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = runner.prefill(prompt, chunk)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        logits[mode] = out
+        res[mode] = {"ttft_s": best, "prefill_tok_per_s": tokens / best}
+        del runner
+        torch.cuda.empty_cache()
+    if "fpv2" in logits and "dense" in logits:
+        a, b = logits["fpv2"], logits["dense"]
+        res["logits_max_abs_diff"] = float((a - b).abs().max())
+        res["top1_agree"] = bool(int(a.argmax()) == int(b.argmax()))
+        res["speedup"] = res["dense"]["ttft_s"] / res["fpv2"]["ttft_s"]
+    return res
