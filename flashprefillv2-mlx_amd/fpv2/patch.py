@@ -41,7 +41,10 @@ except ImportError:  # pragma: no cover - older torch
 _ORIGINAL_SDPA = F.scaled_dot_product_attention
 _enabled = False
 _collect_stats = False
-_selected_counts: list[torch.Tensor] = []
+# Selected blocks of FPV2 calls, summed on each call's device (0-d int64
+# tensors, one per device): accumulating costs one small kernel per call and
+# no host synchronisation; block_sparsity() reads them once.
+_selected_totals: dict[torch.device, torch.Tensor] = {}
 _selected_dense_blocks = 0
 _visible_blocks = 0
 _PACKED_TILE_ROWS = 128
@@ -88,8 +91,7 @@ def block_sparsity() -> float:
     if not _visible_blocks:
         return 0.0
     selected = _selected_dense_blocks
-    if _selected_counts:
-        total = torch.stack([c.sum(dtype=torch.int64) for c in _selected_counts]).sum()
+    for total in _selected_totals.values():
         selected += int(total.item())
     return 1.0 - selected / _visible_blocks
 
@@ -222,7 +224,11 @@ def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out
         _lib.check(status, "score_select")
     if _collect_stats:
         global _visible_blocks
-        _selected_counts.append(counts)
+        total = _selected_totals.get(counts.device)
+        if total is None:
+            total = _selected_totals[counts.device] = torch.zeros(
+                (), dtype=torch.int64, device=counts.device)
+        total += counts.sum(dtype=torch.int64)
         _visible_blocks += _causal_block_count(kv_heads, geo.query_length, geo.offset, config)
     if out is None:
         out = torch.empty((geo.query_heads, geo.query_length, geo.head_dim),
@@ -338,7 +344,7 @@ def enable(
     elif config is None:
         config = FPV2Config(**config_fields)
     _collect_stats = collect_stats
-    _selected_counts.clear()
+    _selected_totals.clear()
     _selected_dense_blocks = 0
     _visible_blocks = 0
 
