@@ -119,7 +119,11 @@ __device__ __forceinline__ void scale_in_place(f32x16& acc, float f) {
 // the two halves of the swap hold x of both lanes of the pair in either order.
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  // plain v_max_f32: the operands are MFMA results or -inf, never signalling
+  // NaNs, so the canonicalising form fmaxf() would add is not needed
+  float m;
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  return m;
 }
 __device__ __forceinline__ float pair_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -431,6 +435,15 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
 #pragma unroll
   for (int i = 0; i < GM::DT; ++i) o[i] = f32x16{};
   float m_ref = neg_inf();
+  // Derived from m_ref, updated only when it changes: the exp2 bias
+  // (-m_ref, 0 while no key has been seen) and the rescale threshold.  The
+  // kernels without correction, and those with D = 256, are at the register
+  // limit and recompute them per slice instead of keeping two more live values.
+  constexpr bool kKeepRef = CORR && D <= 128;
+  float neg_m = 0.f;
+  float m_thr = neg_inf();
+  auto bias_of_ref = [&]() { return kKeepRef ? neg_m : ((m_ref == neg_inf()) ? 0.f : -m_ref); };
+  auto thr_of_ref = [&]() { return kKeepRef ? m_thr : m_ref + kRescaleSlack; };
   float l_run = 0.f;
 
   // LDS read addresses relative to a slice (32 keys of a stage).  K: lane
@@ -541,8 +554,7 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
     }
     float bias = 0.f;
     if constexpr (HP) {
-      const float shift = p_pend.corr ? a.shift : 0.f;
-      bias = shift - ((m_ref == neg_inf()) ? 0.f : m_ref);
+      bias = bias_of_ref() + (p_pend.corr ? a.shift : 0.f);
     }
     u32x4 w[2];
     // P for the pair of keys (2pi, 2pi+1) of the pending slice
@@ -633,10 +645,14 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
 
     // ---- stage C: reference max of the new slice ----
     if constexpr (HN) {
-      if (__ballot(m_cand > m_ref + kRescaleSlack) != 0ull) {
+      if (__ballot(m_cand > thr_of_ref()) != 0ull) {
         const float m_new = fmaxf(m_ref, m_cand);
         const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
         m_ref = m_new;
+        if constexpr (kKeepRef) {
+          neg_m = (m_ref == neg_inf()) ? 0.f : -m_ref;
+          m_thr = m_ref + kRescaleSlack;
+        }
         l_run *= alpha;
 #pragma unroll
         for (int dt = 0; dt < GM::DT; ++dt) scale_in_place(o[dt], alpha);
