@@ -296,33 +296,40 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   const int n_corr = CORR ? (pr_count + BN - 1) / BN : 0;
   const int n_steps = n_sel + n_corr;
 
-  // Block ids of the selected list are read 64 at a time into one VGPR (lane
-  // = list entry) and handed out with readlane; the pruned list likewise, 64
-  // entries per VGPR, handed to the fill lanes with ds_bpermute.  The walk
-  // state (list entry, sub-tile) advances incrementally.
-  int ids_base = 0;
-  int ids_lanes = lane < sel_count ? clampi(ids[lane], 0, Nb - 1) : 0;
+  // Exact steps are described 64 at a time: lane j of a window holds the
+  // first key and valid-row count of step win_base + j, computed in one
+  // vector pass from the selected list, and a step reads its pair with two
+  // readlanes.  Correction steps follow from the step index; the pruned list
+  // is read 64 entries per VGPR and handed to the fill lanes with
+  // ds_bpermute.
+  int win_base = 0, win_key0 = 0, win_nk = 0;
+  auto load_window = [&](int base) {
+    const int it = base + lane;
+    int key0 = 0, nk = 0;
+    if (it < n_sel) {
+      const int li = it / subs;  // < li_end
+      const int sub = it - li * subs;
+      key0 = clampi(ids[li], 0, Nb - 1) * a.bk + sub * BN;
+      const int n = min(min(a.bk - sub * BN, BN), a.Lk - key0);
+      nk = (key0 > abs_last || n < 0) ? 0 : n;
+    }
+    win_key0 = key0;
+    win_nk = nk;
+  };
+  load_window(0);
   int pids_lanes = 0;
   if constexpr (CORR) pids_lanes = lane < pr_count ? clampi(pids[lane], 0, Nb - 1) : 0;
-  int cur_li = 0, cur_sub = 0, walk_it = 0;
+  int walk_it = 0;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
     const int it = walk_it++;
     if (it < n_sel) {
-      if (cur_li - ids_base >= 64) {
-        ids_base += 64;
-        const int li = ids_base + lane;
-        ids_lanes = li < sel_count ? clampi(ids[li], 0, Nb - 1) : 0;
+      if (it - win_base >= 64) {
+        win_base += 64;
+        load_window(win_base);
       }
-      const int blk = __builtin_amdgcn_readlane(ids_lanes, cur_li - ids_base);
-      s.key0 = blk * a.bk + cur_sub * BN;
-      int n = min(min(a.bk - cur_sub * BN, BN), a.Lk - s.key0);
-      if (s.key0 > abs_last) n = 0;
-      s.nkeys = n < 0 ? 0 : n;
-      if (++cur_sub == subs) {
-        cur_sub = 0;
-        ++cur_li;
-      }
+      s.key0 = __builtin_amdgcn_readlane(win_key0, it - win_base);
+      s.nkeys = __builtin_amdgcn_readlane(win_nk, it - win_base);
     } else if (it < n_steps) {
       s.corr = 1;
       s.li = (it - n_sel) * BN;
