@@ -86,12 +86,18 @@ __device__ int block_sum_int(int v, int* red) {
   return r;
 }
 
-// Merge (c, e) pairs: sum of exp(x - c) terms under a common max.
+// Energies are kept in base 2: logits x = s * log2(e), and a block's running
+// (c, e) = (max x, sum 2^(x - c)).  2^(x - m) = exp(s - m / log2(e)), so the
+// energies, their ratios and the selection are those of exp(s - max).
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Merge (c, e) pairs: sum of 2^(x - c) terms under a common max.
 __device__ __forceinline__ void merge_ce(float& c, float& e, float c2, float e2) {
   const float nc = fmaxf(c, c2);
   if (nc == neg_inf()) return;
-  const float a = (c == neg_inf()) ? 0.f : e * expf(c - nc);
-  const float b = (c2 == neg_inf()) ? 0.f : e2 * expf(c2 - nc);
+  const float a = (c == neg_inf()) ? 0.f : e * exp2_fast(c - nc);
+  const float b = (c2 == neg_inf()) ? 0.f : e2 * exp2_fast(c2 - nc);
   c = nc;
   e = a + b;
 }
@@ -166,7 +172,7 @@ __device__ void finish_tile(const SelectArgs& a, const TileInfo& ti, float* cb, 
   float emax = 0.f;
   for (int64_t b = tid; b < ti.nfv; b += kThreads) {
     const float c = cb[b];
-    const float E = (c == neg_inf()) ? 0.f : eb[b] * expf(c - m);
+    const float E = (c == neg_inf()) ? 0.f : eb[b] * exp2_fast(c - m);
     eb[b] = E;
     emax = fmaxf(emax, E);
   }
@@ -212,6 +218,7 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
   __shared__ int ired[8];
   __shared__ int rpos[kRowsPerPass];  // local query position, -1: no such row
   __shared__ int rhead[kRowsPerPass]; // g of the packed row
+  __shared__ int rg_lo[kRowsPerPass / 32], rg_hi[kRowsPerPass / 32];  // per 32-row group
 
   const TileInfo ti = tile_info(a);
   const int tid = threadIdx.x;
@@ -223,6 +230,8 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
   const int64_t n_comp = a.scores ? a.Nb : ti.nfv;
   const uint16_t* pk = static_cast<const uint16_t*>(a.pk) + ti.h * a.pk_hs;
   const uint16_t* qbase = static_cast<const uint16_t*>(a.q);
+  const float sc2 = a.scale * kLog2e;
+  const bool fast_ok = a.scores == nullptr && sc2 > 0.f;
 
   for (int64_t b = tid; b < n_comp; b += kThreads) {
     cb[b] = neg_inf();
@@ -240,6 +249,19 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
       }
       rpos[tid] = p;
       rhead[tid] = gg;
+    }
+    __syncthreads();
+    // Lowest and highest position of each 32-row group (-1 rows make the
+    // group take the checked path).
+    if (tid < kRowsPerPass / 32) {
+      int lo_p = 0x7fffffff, hi_p = -1;
+      for (int r = 0; r < 32; ++r) {
+        const int p = rpos[tid * 32 + r];
+        lo_p = min(lo_p, p);
+        hi_p = max(hi_p, p);
+      }
+      rg_lo[tid] = lo_p;
+      rg_hi[tid] = hi_p;
     }
     // Stage 128 packed rows of Q (zeros past the tile or the valid length).
     for (int e = tid; e < kRowsPerPass * (D / 8); e += kThreads) {
@@ -281,6 +303,21 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
           const u32x4 qv = load16(qs + (rg * 32 + l32) * LDQ + k * 16 + hf * 8);
           acc = Elem<T>::mfma32(as_vec8<T>(qv), kf[k], acc);
         }
+        // Fast path: every row of the group sees block b in every lane (the
+        // blocks before the diagonal), no scores requested, positive scale.
+        const bool all_ok = b_scored && rg_lo[rg] >= lo && rg_hi[rg] < lq;
+        if (fast_ok && __ballot(!all_ok) == 0ull) {
+          float mx = acc[0];
+#pragma unroll
+          for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
+          const float nc = fmaxf(cmax, mx * sc2);
+          float e = (cmax == neg_inf()) ? 0.f : esum * exp2_fast(cmax - nc);
+#pragma unroll
+          for (int j = 0; j < 16; ++j) e += exp2_fast(fmaf(acc[j], sc2, -nc));
+          cmax = nc;
+          esum = e;
+          continue;
+        }
         // Lane holds rows rg*32 + (j/4)*8 + hf*4 + j%4 of block b.
         float s[16];
         bool ok[16];
@@ -289,19 +326,19 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
         for (int j = 0; j < 16; ++j) {
           const int r = rg * 32 + (j >> 2) * 8 + hf * 4 + (j & 3);
           const int pos = rpos[r];
-          s[j] = acc[j] * a.scale;
           if (a.scores && pos >= 0 && b < a.Nb)
-            a.scores[((ti.h * a.G + rhead[r]) * a.Lq_pad + pos) * a.Nb + b] = s[j];
+            a.scores[((ti.h * a.G + rhead[r]) * a.Lq_pad + pos) * a.Nb + b] = acc[j] * a.scale;
+          s[j] = acc[j] * sc2;
           const bool valid = b_scored && pos >= lo && pos < lq;
           ok[j] = valid;
           if (valid) lm = fmaxf(lm, s[j]);
         }
         if (lm != neg_inf()) {
           const float nc = fmaxf(cmax, lm);
-          float e = (cmax == neg_inf()) ? 0.f : esum * expf(cmax - nc);
+          float e = (cmax == neg_inf()) ? 0.f : esum * exp2_fast(cmax - nc);
 #pragma unroll
           for (int j = 0; j < 16; ++j)
-            if (ok[j]) e += expf(s[j] - nc);
+            if (ok[j]) e += exp2_fast(s[j] - nc);
           cmax = nc;
           esum = e;
         }
@@ -386,7 +423,7 @@ __global__ __launch_bounds__(kThreads) void select_generic_kernel(SelectArgs a, 
         const int64_t g = pr / a.tq;
         const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
         if (a.scores) a.scores[((ti.h * a.G + g) * a.Lq_pad + pos) * a.Nb + b] = s;
-        if (pos < a.Lq && b < ti.nfv && b * a.bk <= a.offset + pos) merge_ce(c, e, s, 1.f);
+        if (pos < a.Lq && b < ti.nfv && b * a.bk <= a.offset + pos) merge_ce(c, e, s * kLog2e, 1.f);
       }
       cb[b] = c;
       eb[b] = e;
