@@ -505,6 +505,13 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
 #define FPV2_MAX_DELAY 0
 #endif
   constexpr int kExpLead = FPV2_EXP_LEAD;   // exp pairs issued before the first QK MFMA
+#ifndef FPV2_EXP_A
+#define FPV2_EXP_A 6
+#endif
+  // exp pairs of the pending slice in stage A; the rest (keys 16-31, the
+  // second P operand) are spread over the first half of the PV MFMAs
+  constexpr int kExpA = FPV2_EXP_A;
+  static_assert(kExpA >= 4 && kExpA <= 8, "the first P operand is built in stage A");
   constexpr int kMaxDelay = FPV2_MAX_DELAY; // PV MFMAs issued before the first row-max step
   constexpr int PER_BATCH = 4;        // MFMA operands per batch of 8 transposing reads
   constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
@@ -583,6 +590,7 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
       // kExpLead pairs first, while the first K fragments are in flight,
       // then the rest spread over the QK MFMAs.
       constexpr int E0 = HP ? kExpLead : 0;
+      constexpr int EA = kExpA;
       if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
       StaticFor<0, GM::KS>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -591,14 +599,15 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
         s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
         if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
         if constexpr (HP)
-          StaticFor<E0 + i * (8 - E0) / GM::KS, E0 + (i + 1) * (8 - E0) / GM::KS>::run(exp_pair);
+          StaticFor<E0 + i * (EA - E0) / GM::KS, E0 + (i + 1) * (EA - E0) / GM::KS>::run(exp_pair);
       });
     } else if constexpr (HP) {
       StaticFor<0, 8>::run(exp_pair);
     }
+    constexpr int EB = HN ? kExpA : 8;  // pairs done once stage A ends
     if constexpr (HP) {
       pb[0] = as_vec8<T>(w[0]);
-      pb[1] = as_vec8<T>(w[1]);
+      if constexpr (EB == 8) pb[1] = as_vec8<T>(w[1]);
     }
 
     // mask of the new slice (diagonal / partial slices only)
@@ -639,6 +648,10 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
             const u32x2(&r)[8] = vb[b & 1];
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
             o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
+            if constexpr (EB < 8 && op < GM::DT) {
+              StaticFor<EB + op * (8 - EB) / GM::DT, EB + (op + 1) * (8 - EB) / GM::DT>::run(exp_pair);
+              if constexpr (op + 1 == GM::DT) pb[1] = as_vec8<T>(w[1]);
+            }
             // the row max starts kMaxDelay MFMAs in, when S^T has landed
             constexpr int DM = kMaxDelay < PV_OPS ? kMaxDelay : PV_OPS - 1;
             if constexpr (HN && op >= DM)
