@@ -472,11 +472,15 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
   // stages, one process() call apart, so that every stage pairs MFMA work
   // with VALU work of another slice:
-  //   A: S^T = K . Q^T of slice n       ||  exp2 / pack / row sum of slice n-1
-  //   B: O^T += V^T . P^T of slice n-1  ||  mask and row max of slice n
+  //   A: S^T = K . Q^T of slice n       ||  exp2 / pack / row sum of 6 of
+  //                                          the 8 key pairs of slice n-1
+  //   B: O^T += V^T . P^T of slice n-1  ||  the last 2 key pairs (during the
+  //                                          MFMAs on the first P operand),
+  //                                          mask and row max of slice n
   //   C: (rare) rescale of O and l when slice n raises the reference max.
   // A wave keeps its matrix pipe busy during its own softmax; the order of
-  // issue within A and B is fixed with scheduling-group barriers.
+  // issue within A and B is fixed in source order, each piece of VALU work
+  // consumed by an empty asm statement so the compiler cannot regroup it.
   struct Slice {
     int corr;       // pooled correction rows (logit shift, no causal mask)
     int key0;       // first key (exact slices)
