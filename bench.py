@@ -144,7 +144,7 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
         stage["attention"] += ev["attention"].elapsed_time(ev["done"])
     stage = {k_: v_ / steps for k_, v_ in stage.items()}
     keep = {}
-    _fpv2_sdpa(q4, k4, v4, scale=scale, config=config, keep=keep)
+    out = _fpv2_sdpa(q4, k4, v4, scale=scale, config=config, keep=keep)
     torch.cuda.synchronize()
     f_ret, sel_frac = retained_flops(keep, seq, torch)
     f_dense = dense_flops(seq)
@@ -170,7 +170,7 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
     res["hbm_frac_pool"] = res["pool_gbs"] / PEAK_HBM_GBS
     log(f"seq {seq}: {ms_step:.3f} ms/layer  stages {json.dumps({k_: round(v_, 4) for k_, v_ in stage.items()})}"
         f"  density {res['density']:.4f}  attn {res['retained_tflops_attention']:.1f} TFLOP/s")
-    data = (q, k, v, keep)
+    data = (q, k, v, keep, out)
     return res, data
 
 
@@ -181,7 +181,7 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
 
     from oracle import fpv2_oracle as orc
 
-    q, k, v, keep = data
+    q, k, v, keep, out_dev = data
     cfg = keep["config"]
     tq = cfg.tile_q
     cores = len(os.sched_getaffinity(0))
@@ -195,25 +195,46 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
     def sample(n_tiles):
         rows0 = seq - n_tiles * tq
         qs = q[:, rows0:].float().cpu().numpy()
+        ids, counts, pids, pcounts = (x[:, nt - n_tiles:] for x in keep["lists"])
+        # the device's selection of the sampled tiles as a mask
+        ids_np, counts_np = ids.cpu().numpy(), counts.cpu().numpy()
+        dev_sel = np.zeros(ids_np.shape, dtype=bool)
+        for h in range(ids_np.shape[0]):
+            for t in range(ids_np.shape[1]):
+                dev_sel[h, t, ids_np[h, t, :counts_np[h, t]]] = True
         t0 = time.perf_counter()
         with threadpool_limits(limits=cores):
-            sel, _ = orc.block_scores_and_select(
+            sel, _, ratio = orc.block_scores_and_select(
                 qs, pooled_k, scale=D ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
-                offset=rows0, query_length=n_tiles * tq)
-            # attention for the sampled rows: the oracle on [Hq, rows, D] with offset
+                offset=rows0, query_length=n_tiles * tq, return_ratio=True)
+            # attention for the sampled rows on the device's selection (the same
+            # work as on the oracle's own), so the output compares like for like
             out = orc.fpv2_attention_blockwise(
-                qs, kn, vn, scale=D ** -0.5, selected=sel, pooled_k=pooled_k,
+                qs, kn, vn, scale=D ** -0.5, selected=dev_sel, pooled_k=pooled_k,
                 pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
         dt = time.perf_counter() - t0
-        ids, counts, pids, pcounts = (x[:, nt - n_tiles:] for x in keep["lists"])
         sub = dict(keep, offset=rows0, lists=(ids, counts, pids, pcounts))
         flops, _ = retained_flops(sub, n_tiles * tq, torch)
-        return dt, flops, out
+        decided = np.abs(ratio - cfg.alpha) > 1e-4
+        diff = np.abs(out_dev[0, :, rows0:].float().cpu().numpy().astype(np.float64) - out)
+        parity = {
+            "tiles": n_tiles,
+            "rows": n_tiles * tq,
+            "block_decisions": int(decided.sum()),
+            "block_mismatches_outside_band": int((sel[decided] != dev_sel[decided]).sum()),
+            "max_abs": float(diff.max()),
+            "mean_abs": float(diff.mean()),
+            "tolerance": {"max_abs": 2e-2, "mean_abs": 2e-3, "band": 1e-4},
+        }
+        parity["pass"] = (parity["block_mismatches_outside_band"] == 0
+                          and parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3)
+        return dt, flops, parity
 
     dt1, f1, _ = sample(1)
     n = max(1, min(nt, int(budget_s / max(dt1, 1e-3))))
     log(f"cpu baseline: 1 tile took {dt1:.2f} s; timing the last {n} tiles")
-    dt, flops, _ = sample(n)
+    dt, flops, parity = sample(n)
+    log(f"parity of the sampled tiles against the oracle: {json.dumps(parity)}")
     return {
         "value": flops / dt / 1e12,
         "unit": "TFLOP/s",
@@ -222,6 +243,7 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
         "sample": (f"numpy oracle (float32, BLAS matmuls on {cores} threads): selection + "
                    f"attention of the last {n} query tiles ({n * tq} rows x {HQ} heads) of "
                    f"the seq-{seq} alpha-{alpha} layer; {dt:.1f} s for {flops:.3e} retained FLOP"),
+        "parity": parity,
     }
 
 

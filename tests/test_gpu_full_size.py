@@ -1,0 +1,71 @@
+"""Parity at BASELINE's full sizes on a sample of query tiles.
+
+The hook runs the whole layer (Qwen3-4B geometry, BASELINE generator) on the
+GPU at seq 32768 and 131072; the oracle then evaluates the last few query
+tiles from the same inputs and the device's pooled keys:
+  * block lists of those tiles bit-exact against the oracle's selection,
+    excluding blocks whose energy ratio lies within 1e-4 of alpha;
+  * their attention rows within max-abs 2e-2 / mean-abs 2e-3 of the oracle's
+    blockwise float32 evaluation on the device's selection.
+Rows are independent, so the last tiles (the longest rows, the dense tail
+and the most blocks) check the full-length walk without evaluating the whole
+layer on the CPU.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import attention_errors, to_np
+from oracle import fpv2_oracle as orc
+from fpv2 import FPV2Config
+from fpv2.patch import _fpv2_sdpa
+from fpv2.synthetic import baseline_qkv
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS, BAND = 2e-2, 2e-3, 1e-4
+
+
+def _device_mask(ids, counts, tiles, num_blocks):
+    ids, counts = to_np(ids[:, tiles]), to_np(counts[:, tiles])
+    mask = np.zeros(ids.shape[:2] + (num_blocks,), dtype=bool)
+    for h in range(ids.shape[0]):
+        for t in range(ids.shape[1]):
+            mask[h, t, ids[h, t, :counts[h, t]]] = True
+    return mask
+
+
+@pytest.mark.parametrize(("seq", "heavy", "n_tiles"), [(32768, 0.06, 6), (131072, 0.03, 3)])
+def test_last_tiles_match_oracle_at_full_size(cuda, seq, heavy, n_tiles):
+    q, k, v = baseline_qkv(seq, planted=3.0, heavy_fraction=heavy, seed=0, device=cuda)
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    keep = {}
+    out = _fpv2_sdpa(q[None], k[None], v[None], scale=128 ** -0.5, config=config, keep=keep)
+    torch.cuda.synchronize()
+    cfg = keep["config"]
+    tq = cfg.tile_q
+    nt = seq // tq
+    rows0 = seq - n_tiles * tq
+    ids, counts, _, _ = keep["lists"]
+    num_blocks = ids.shape[-1]
+    dev_sel = _device_mask(ids, counts, slice(nt - n_tiles, nt), num_blocks)
+
+    ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
+    pooled_k = to_np(keep["pooled_k"])
+    pooled_v = to_np(keep["pooled_v"])
+    qs = to_np(q[:, rows0:])
+    sel, _, ratio = orc.block_scores_and_select(
+        qs, pooled_k, scale=128 ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
+        offset=rows0, query_length=n_tiles * tq, return_ratio=True)
+    decided = np.abs(ratio - cfg.alpha) > BAND
+    assert np.array_equal(sel[decided], dev_sel[decided])
+    assert dev_sel.sum() > 0
+
+    ref = orc.fpv2_attention_blockwise(
+        qs, to_np(k), to_np(v), scale=128 ** -0.5, selected=dev_sel, pooled_k=pooled_k,
+        pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
+    err = attention_errors(to_np(out[0, :, rows0:]), ref)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
