@@ -38,9 +38,16 @@ def _device_mask(ids, counts, tiles, num_blocks):
     return mask
 
 
-@pytest.mark.parametrize(("seq", "heavy", "n_tiles"), [(32768, 0.06, 6), (131072, 0.03, 3)])
-def test_last_tiles_match_oracle_at_full_size(cuda, seq, heavy, n_tiles):
-    q, k, v = baseline_qkv(seq, planted=3.0, heavy_fraction=heavy, seed=0, device=cuda)
+@pytest.mark.parametrize(("seq", "heavy", "planted", "n_tiles", "skip"), [
+    (32768, 0.06, 3.0, 6, 0),
+    (131072, 0.03, 3.0, 3, 0),
+    # the bench's contrast variant: planted x 3*sqrt(D) prunes most blocks, so
+    # the correction phase carries hundreds of pooled rows per tile; the tiles
+    # just before the dense tail (the last 2 tiles) are sampled
+    (131072, 0.03, 3.0 * 128 ** 0.5, 3, 2),
+])
+def test_last_tiles_match_oracle_at_full_size(cuda, seq, heavy, planted, n_tiles, skip):
+    q, k, v = baseline_qkv(seq, planted=planted, heavy_fraction=heavy, seed=0, device=cuda)
     config = FPV2Config(alpha=0.1, sink_tokens=128)
     keep = {}
     out = _fpv2_sdpa(q[None], k[None], v[None], scale=128 ** -0.5, config=config, keep=keep)
@@ -48,24 +55,28 @@ def test_last_tiles_match_oracle_at_full_size(cuda, seq, heavy, n_tiles):
     cfg = keep["config"]
     tq = cfg.tile_q
     nt = seq // tq
-    rows0 = seq - n_tiles * tq
+    rows0 = seq - (n_tiles + skip) * tq
     ids, counts, _, _ = keep["lists"]
     num_blocks = ids.shape[-1]
-    dev_sel = _device_mask(ids, counts, slice(nt - n_tiles, nt), num_blocks)
+    dev_sel = _device_mask(ids, counts, slice(nt - n_tiles - skip, nt - skip), num_blocks)
 
     ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
+    if skip:  # the sampled tiles are not the call's last ones: no dense tail among them
+        ocfg = orc._replace(ocfg, last_n_blocks=0)
     pooled_k = to_np(keep["pooled_k"])
     pooled_v = to_np(keep["pooled_v"])
-    qs = to_np(q[:, rows0:])
+    qs = to_np(q[:, rows0:rows0 + n_tiles * tq])
     sel, _, ratio = orc.block_scores_and_select(
         qs, pooled_k, scale=128 ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
         offset=rows0, query_length=n_tiles * tq, return_ratio=True)
     decided = np.abs(ratio - cfg.alpha) > BAND
     assert np.array_equal(sel[decided], dev_sel[decided])
     assert dev_sel.sum() > 0
+    if planted > 3.0:
+        assert dev_sel.mean() < 0.5  # sparse: the correction phase is exercised
 
     ref = orc.fpv2_attention_blockwise(
         qs, to_np(k), to_np(v), scale=128 ** -0.5, selected=dev_sel, pooled_k=pooled_k,
         pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
-    err = attention_errors(to_np(out[0, :, rows0:]), ref)
+    err = attention_errors(to_np(out[0, :, rows0:rows0 + n_tiles * tq]), ref)
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
