@@ -207,7 +207,7 @@ __device__ void finish_tile(const SelectArgs& a, const TileInfo& ti, float* cb, 
 // LDS: Q pass [128][D+8] (reused for the flag arrays), c_b[Nb], e_b[Nb].
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
+__global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_mfma_kernel(SelectArgs a) {
   constexpr int LDQ = D + 8;  // padded row: conflict-free 16-byte column reads
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
   extern __shared__ __align__(16) unsigned char smem[];
@@ -280,6 +280,13 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
     __syncthreads();
     const int64_t rows_here = (R - rc) < kRowsPerPass ? (R - rc) : kRowsPerPass;
     const int nrg = static_cast<int>((rows_here + 31) / 32);
+    // Lowest / highest row position of the pass (wave-uniform).
+    int pass_lo = 0x7fffffff, pass_hi = -1;
+    for (int rg = 0; rg < nrg; ++rg) {
+      pass_lo = min(pass_lo, rg_lo[rg]);
+      pass_hi = max(pass_hi, rg_hi[rg]);
+    }
+    const int lq = static_cast<int>(a.Lq);
 
     for (int64_t chunk = wave; chunk * 32 < n_comp; chunk += 4) {
       const int64_t b = chunk * 32 + l32;
@@ -287,7 +294,6 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
       const bool b_scored = b < ti.nfv;
       int64_t lo64 = b * a.bk - a.offset;
       const int lo = lo64 < 0 ? 0 : static_cast<int>(lo64 > 0x7fffffff ? 0x7fffffff : lo64);
-      const int lq = static_cast<int>(a.Lq);
       typename Elem<T>::vec8 kf[KS];
 #pragma unroll
       for (int k = 0; k < KS; ++k) {
@@ -296,27 +302,50 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
         kf[k] = as_vec8<T>(v);
       }
       float cmax = neg_inf(), esum = 0.f;
+      // Fast path: every row of the pass sees the lane's block in every lane
+      // (the chunks before the diagonal), no scores requested, positive
+      // scale: no per-row tests.  The next row group's Q fragments are read
+      // from LDS while the current group's energies are summed.
+      const bool all_ok = b_scored && pass_lo >= lo && pass_hi < lq;
+      if (fast_ok && __ballot(!all_ok) == 0ull) {
+        u32x4 qv[2][KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qv[0][k] = load16(qs + l32 * LDQ + k * 16 + hf * 8);
+        for (int rg = 0; rg < nrg; rg += 2) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int g = rg + half;
+            if (g < nrg) {
+              f32x16 acc = {};
+#pragma unroll
+              for (int k = 0; k < KS; ++k) acc = Elem<T>::mfma32(as_vec8<T>(qv[half][k]), kf[k], acc);
+              if (g + 1 < nrg) {
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                  qv[half ^ 1][k] = load16(qs + ((g + 1) * 32 + l32) * LDQ + k * 16 + hf * 8);
+              }
+              float mx = acc[0];
+#pragma unroll
+              for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
+              const float nc = fmaxf(cmax, mx * sc2);
+              float e0 = (cmax == neg_inf()) ? 0.f : esum * exp2_fast(cmax - nc), e1 = 0.f;
+#pragma unroll
+              for (int j = 0; j < 16; j += 2) {
+                e0 += exp2_fast(fmaf(acc[j], sc2, -nc));
+                e1 += exp2_fast(fmaf(acc[j + 1], sc2, -nc));
+              }
+              cmax = nc;
+              esum = e0 + e1;
+            }
+          }
+        }
+      } else {
       for (int rg = 0; rg < nrg; ++rg) {
         f32x16 acc = {};
 #pragma unroll
         for (int k = 0; k < KS; ++k) {
           const u32x4 qv = load16(qs + (rg * 32 + l32) * LDQ + k * 16 + hf * 8);
           acc = Elem<T>::mfma32(as_vec8<T>(qv), kf[k], acc);
-        }
-        // Fast path: every row of the group sees block b in every lane (the
-        // blocks before the diagonal), no scores requested, positive scale.
-        const bool all_ok = b_scored && rg_lo[rg] >= lo && rg_hi[rg] < lq;
-        if (fast_ok && __ballot(!all_ok) == 0ull) {
-          float mx = acc[0];
-#pragma unroll
-          for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
-          const float nc = fmaxf(cmax, mx * sc2);
-          float e = (cmax == neg_inf()) ? 0.f : esum * exp2_fast(cmax - nc);
-#pragma unroll
-          for (int j = 0; j < 16; ++j) e += exp2_fast(fmaf(acc[j], sc2, -nc));
-          cmax = nc;
-          esum = e;
-          continue;
         }
         // Lane holds rows rg*32 + (j/4)*8 + hf*4 + j%4 of block b.
         float s[16];
@@ -343,6 +372,7 @@ __global__ __launch_bounds__(kThreads) void select_mfma_kernel(SelectArgs a) {
           esum = e;
         }
       }
+      }  // checked path
       // Partner lane (hf ^ 1) holds the other 16 rows of each row group.
       const float oc = __shfl_xor(cmax, 32);
       const float oe = __shfl_xor(esum, 32);
