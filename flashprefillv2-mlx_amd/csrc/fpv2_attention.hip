@@ -201,17 +201,22 @@ struct Step {
   int nkeys;  // valid rows in the sub-tile
 };
 
-template <typename T, int D, bool CORR, int WAVES, int NST, int BNK>
-__global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
+// DS = 2: two waves share each 32-row group, each owning half of the head
+// dimension of O (both compute the full S and P); this keeps D = 256 at two
+// waves per SIMD within 256 registers.
+template <typename T, int D, bool CORR, int WAVES, int NST, int BNK, int DS = 1>
+__global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D, BNK>;
   static_assert(BNK == 32 || BNK == 64, "sub-tiles of 32 or 64 keys");
-  // asm LDS reads for D <= 128; D = 256 needs more registers than a wave has
-  // and lets the compiler schedule its LDS reads (see lds_read_b128).
-  constexpr bool kAsm = D <= 128;
+  static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0), "D split in halves");
+  // asm LDS reads unless a wave's registers do not hold them (D = 256 without
+  // the split), where the compiler schedules its LDS reads (see lds_read_b128).
+  constexpr bool kAsm = D <= 128 || DS == 2;
+  constexpr int DT = GM::DT / DS;  // 32-wide output column tiles of this wave
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = GM::BN;
   constexpr int ROWB = GM::ROWB;
-  constexpr int RW = WAVES * 32;          // packed query rows per workgroup
+  constexpr int RW = WAVES / DS * 32;     // packed query rows per workgroup
   constexpr int NIK = GM::JT / WAVES;     // fill instructions per wave per sub-tile
   constexpr int NI = 2 * NIK;             // ... per stage (K then V)
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
@@ -236,7 +241,9 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
 
   // ---- this lane's query row ----
   const int R = a.G * a.tq;
-  const int prow = chunk * RW + wave * 32 + l32;
+  const int rwave = wave % (WAVES / DS);  // row group of this wave
+  const int dhalf = wave / (WAVES / DS);  // part of the head dimension (DS = 2)
+  const int prow = chunk * RW + rwave * 32 + l32;
   const bool exists = prow < R;
   int g = 0, pos = 0;
   if (exists) {
@@ -438,9 +445,9 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   // O / l are rescaled only when some row's max grows past that, so the
   // common case costs no rescale at all.  The result O / l is unchanged.
   constexpr float kRescaleSlack = 8.0f;
-  f32x16 o[GM::DT];
+  f32x16 o[DT];
 #pragma unroll
-  for (int i = 0; i < GM::DT; ++i) o[i] = f32x16{};
+  for (int i = 0; i < DT; ++i) o[i] = f32x16{};
   float m_ref = neg_inf();
   // Derived from m_ref, updated only when it changes: the exp2 bias
   // (-m_ref, 0 while no key has been seen) and the rescale threshold.  The
@@ -465,8 +472,11 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   const int tr_row = (lane & 15) >> 2;
   const int cig = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // chunk within a 64-byte group
   const int vq = ROWB >= 256 ? tr_row : ((tr_row >> 1) & 1);   // swizzled 64-byte group
+  // (DS = 2: the second half of D lies 64*DT bytes further along each row,
+  // above the swizzled bits)
   const uint32_t vbase =
-      smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8;
+      (smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8) ^
+      static_cast<uint32_t>(dhalf * DT * 64);
 
   // ---- slice pipeline ----
   // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
@@ -500,7 +510,7 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   f32x16 s_buf[2] = {f32x16{}, f32x16{}};
   Slice p_pend{0, 0, 0, 0u};
 
-  constexpr int PV_OPS = 2 * GM::DT;  // PV MFMAs per slice: (u, dt)
+  constexpr int PV_OPS = 2 * DT;  // PV MFMAs per slice: (u, dt)
   // issue-order tuning of the slice pipeline (see process_m)
 #ifndef FPV2_EXP_LEAD
 #define FPV2_EXP_LEAD 0
@@ -525,7 +535,7 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
       constexpr int q = decltype(qc)::value;
       constexpr int op = b * PER_BATCH + q;
       if constexpr (op < PV_OPS) {
-        constexpr int u = op / GM::DT, dt = op % GM::DT;
+        constexpr int u = op / DT, dt = op % DT;
         const uint32_t addr = va ^ (64 * dt);
         r[2 * q] = lds_read_tr<kAsm, u * 16 * ROWB>(addr);
         r[2 * q + 1] = lds_read_tr<kAsm, (u * 16 + 8) * ROWB>(addr);
@@ -648,13 +658,13 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
           constexpr int q = decltype(qc)::value;
           constexpr int op = b * PER_BATCH + q;
           if constexpr (op < PV_OPS) {
-            constexpr int u = op / GM::DT, dt = op % GM::DT;
+            constexpr int u = op / DT, dt = op % DT;
             const u32x2(&r)[8] = vb[b & 1];
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
             o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-            if constexpr (EB < 8 && op < GM::DT) {
-              StaticFor<EB + op * (8 - EB) / GM::DT, EB + (op + 1) * (8 - EB) / GM::DT>::run(exp_pair);
-              if constexpr (op + 1 == GM::DT) pb[1] = as_vec8<T>(w[1]);
+            if constexpr (EB < 8 && op < DT) {
+              StaticFor<EB + op * (8 - EB) / DT, EB + (op + 1) * (8 - EB) / DT>::run(exp_pair);
+              if constexpr (op + 1 == DT) pb[1] = as_vec8<T>(w[1]);
             }
             // the row max starts kMaxDelay MFMAs in, when S^T has landed
             constexpr int DM = kMaxDelay < PV_OPS ? kMaxDelay : PV_OPS - 1;
@@ -685,7 +695,7 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
         }
         l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < GM::DT; ++dt) scale_in_place(o[dt], alpha);
+        for (int dt = 0; dt < DT; ++dt) scale_in_place(o[dt], alpha);
       }
       p_pend = nw;
     }
@@ -769,10 +779,10 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   const float inv = (row_valid && l_tot > 0.f) ? 1.f / l_tot : 0.f;
   uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g) * a.o_hs + pos * a.o_rs;
 #pragma unroll
-  for (int dt = 0; dt < GM::DT; ++dt) {
+  for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
-      const int d0 = dt * 32 + jg * 8 + hf * 4;
+      const int d0 = (dhalf * DT + dt) * 32 + jg * 8 + hf * 4;
       u32x2 w;
       w[0] = pack2<T>(o[dt][jg * 4 + 0] * inv, o[dt][jg * 4 + 1] * inv);
       w[1] = pack2<T>(o[dt][jg * 4 + 2] * inv, o[dt][jg * 4 + 3] * inv);
@@ -781,10 +791,11 @@ __global__ __launch_bounds__(WAVES * 64, (D <= 128 ? 2 : 1)) void sparse_attn_ke
   }
 }
 
-template <typename T, int D, bool CORR, int WAVES, int NST, int BNK>
+template <typename T, int D, bool CORR, int WAVES, int NST, int BNK, int DS = 1>
 int launch_attn(AttnArgs a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, BNK>;
-  a.nchunk = (a.G * a.tq + WAVES * 32 - 1) / (WAVES * 32);
+  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, BNK, DS>;
+  constexpr int RW = WAVES / DS * 32;
+  a.nchunk = (a.G * a.tq + RW - 1) / RW;
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
   if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
   hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(WAVES * 64), 0, stream, a);
@@ -794,7 +805,8 @@ int launch_attn(AttnArgs a, hipStream_t stream) {
 // Workgroup shape.  D <= 128: 8 waves (256 rows) over 64-key sub-tiles in a
 // 4-stage ring (128 KiB, one workgroup per CU) when the packed rows of a tile
 // come in multiples of 256; else 4 waves (128 rows) over 32-key sub-tiles in
-// a 4-stage ring (64 KiB, two workgroups per CU).  D = 256: 4 waves, 32-key
+// a 4-stage ring (64 KiB, two workgroups per CU).  D = 256: 8 waves for 128
+// rows, two per 32-row group each owning half of D (DS = 2), 32-key
 // sub-tiles, 128 KiB.
 template <typename T, int D, bool CORR>
 int launch_shape(const AttnArgs& a, hipStream_t s) {
@@ -802,7 +814,7 @@ int launch_shape(const AttnArgs& a, hipStream_t s) {
     if ((static_cast<int64_t>(a.G) * a.tq) % 256 == 0) return launch_attn<T, D, CORR, 8, 4, 64>(a, s);
     return launch_attn<T, D, CORR, 4, 4, 32>(a, s);
   } else {
-    return launch_attn<T, D, CORR, 4, 4, 32>(a, s);
+    return launch_attn<T, D, CORR, 8, 4, 32, 2>(a, s);
   }
 }
 
