@@ -202,8 +202,9 @@ struct Step {
 };
 
 // DS = 2: two waves share each 32-row group, each owning half of the head
-// dimension of O (both compute the full S and P); this keeps D = 256 at two
-// waves per SIMD within 256 registers.
+// dimension: each multiplies its half of Q and K into a partial S, the two
+// partials are summed through LDS, both compute P, and each accumulates its
+// half of O.  This keeps D = 256 at two waves per SIMD within 256 registers.
 template <typename T, int D, bool CORR, int WAVES, int NST, int BNK, int DS = 1>
 __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D, BNK>;
@@ -213,6 +214,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // the split), where the compiler schedules its LDS reads (see lds_read_b128).
   constexpr bool kAsm = D <= 128 || DS == 2;
   constexpr int DT = GM::DT / DS;  // 32-wide output column tiles of this wave
+  constexpr int KSQ = GM::KS / DS; // 16-deep QK k-steps of this wave
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = GM::BN;
   constexpr int ROWB = GM::ROWB;
@@ -222,6 +224,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
   static_assert(NST >= 2 && NI * (NST - 2) <= 63, "vmcnt range");
   __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE];
+  // DS = 2: each wave's partial S (64 lanes x 16 floats) for its partner
+  __shared__ __align__(16) uint8_t xbuf[DS == 2 ? WAVES * 4096 : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -253,7 +257,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const bool row_valid = exists && pos < a.Lq;
   const int qpos_abs = a.offset + pos;
 
-  vec8 qf[GM::KS];
+  vec8 qf[KSQ];
   {
     const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
     const uint32_t qoff =
@@ -263,8 +267,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // factor: for scale < 0 the queries are negated instead (s*c = (-s)*(-c)).
     const uint32_t sign = a.c_scale < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int k = 0; k < GM::KS; ++k) {
-      u32x4 v = buf_load16(qr, qoff + (row_valid ? k * 32 : 0));
+    for (int k = 0; k < KSQ; ++k) {
+      u32x4 v = buf_load16(qr, qoff + (row_valid ? (dhalf * KSQ + k) * 32 : 0));
       v ^= sign;
       qf[k] = as_vec8<T>(v);
     }
@@ -468,7 +472,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // (16u (+8)) * ROWB.  The XOR terms only touch bits below 9, and slice
   // offsets are multiples of 32 rows, so slice offsets add outside the XOR.
   const int km = GM::kmask(l32);
-  const uint32_t kbase = smem_lds + l32 * ROWB + ((16 * hf) ^ (16 * km));
+  // (DS = 2: this wave's k-steps start 32*KSQ bytes along the row, above
+  // the swizzled bits)
+  const uint32_t kbase =
+      (smem_lds + l32 * ROWB + ((16 * hf) ^ (16 * km))) ^ static_cast<uint32_t>(dhalf * KSQ * 32);
   const int tr_row = (lane & 15) >> 2;
   const int cig = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // chunk within a 64-byte group
   const int vq = ROWB >= 256 ? tr_row : ((tr_row >> 1) & 1);   // swizzled 64-byte group
@@ -558,11 +565,11 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     constexpr bool MASK = decltype(mask_c)::value;
     f32x16& s_new = s_buf[B];
     f32x16& s_old = s_buf[1 - B];
-    constexpr int KW = GM::KS < 4 ? GM::KS : 4;  // K fragment reads in flight
+    constexpr int KW = KSQ < 4 ? KSQ : 4;  // K fragment reads in flight
     const uint32_t va = vbase + p_pend.off;
     const uint32_t ka = kbase + nw.off;
     u32x2 vb[2][8];
-    u32x4 kf[GM::KS];
+    u32x4 kf[KSQ];
     vec8 pb[2];
 
     // ---- stage A ----
@@ -606,14 +613,14 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       constexpr int E0 = HP ? kExpLead : 0;
       constexpr int EA = kExpA;
       if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
-      StaticFor<0, GM::KS>::run([&](auto ic) {
+      StaticFor<0, KSQ>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        constexpr int younger = (GM::KS - 1 - i) < (KW - 1) ? (GM::KS - 1 - i) : (KW - 1);
+        constexpr int younger = (KSQ - 1 - i) < (KW - 1) ? (KSQ - 1 - i) : (KW - 1);
         lgkm_wait<kAsm, younger>(kf[i]);
         s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
-        if constexpr (i + KW < GM::KS) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
+        if constexpr (i + KW < KSQ) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
         if constexpr (HP)
-          StaticFor<E0 + i * (EA - E0) / GM::KS, E0 + (i + 1) * (EA - E0) / GM::KS>::run(exp_pair);
+          StaticFor<E0 + i * (EA - E0) / KSQ, E0 + (i + 1) * (EA - E0) / KSQ>::run(exp_pair);
       });
     } else if constexpr (HP) {
       StaticFor<0, 8>::run(exp_pair);
@@ -622,6 +629,24 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     if constexpr (HP) {
       pb[0] = as_vec8<T>(w[0]);
       if constexpr (EB == 8) pb[1] = as_vec8<T>(w[1]);
+    }
+
+    // DS = 2: add the partner's partial S (every wave of the workgroup takes
+    // this path in the same calls, so the barrier is uniform; the next write
+    // follows the next sub-tile's barrier, after the partner's read)
+    if constexpr (HN && DS == 2) {
+      f32x4* mine = reinterpret_cast<f32x4*>(xbuf + wave * 4096) + lane;
+      const f32x4* theirs = reinterpret_cast<const f32x4*>(xbuf + (wave ^ (WAVES / 2)) * 4096) + lane;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        mine[j * 64] = f32x4{s_new[4 * j], s_new[4 * j + 1], s_new[4 * j + 2], s_new[4 * j + 3]};
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 v = theirs[j * 64];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_new[4 * j + e] += v[e];
+      }
     }
 
     // mask of the new slice (diagonal / partial slices only)
