@@ -276,24 +276,50 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const float c_pos = fmaxf(fabsf(a.c_scale), 1e-30f);
 
   // ---- block lists of (h, t), clipped as kernel.py:555-558 ----
+  // The counts and the first 64 entries of both lists are requested together
+  // (one memory round trip, alongside Q); the walk's set-up below reads them
+  // from registers, so a workgroup with short lists starts filling after two
+  // round trips instead of one per dependent step.
   const int Nb = a.Nb;
   const int64_t list_row = static_cast<int64_t>(h) * a.Nt + t;
   const int32_t* ids = a.ids + list_row * Nb;
   const int32_t* pids = a.pids + list_row * Nb;
-  const int sel_count = clampi(a.counts[list_row], 0, Nb);
-  const int pr_count = CORR ? clampi(a.pcounts[list_row], 0, Nb) : 0;
+  const int cnt_raw = a.counts[list_row];
+  const int pcnt_raw = CORR ? a.pcounts[list_row] : 0;
+  const int id_lane = clampi(ids[min(lane, Nb - 1)], 0, Nb - 1);  // entry `lane`
+  const int pid_lane = CORR ? clampi(pids[min(lane, Nb - 1)], 0, Nb - 1) : 0;
+  const int sel_count = clampi(cnt_raw, 0, Nb);
+  const int pr_count = CORR ? clampi(pcnt_raw, 0, Nb) : 0;
   const int subs = (a.bk + BN - 1) / BN;
 
   // The walk stops at the first listed block that starts after the tile's
-  // last row (kernel.py:252): find it with one ballot per 64 entries.
+  // last row (kernel.py:252): one ballot per 64 entries, the first 64 from
+  // registers, later ones four loads at a time.
   int li_end = sel_count;
-  for (int base = 0; base < sel_count; base += 64) {
-    const int li = base + lane;
-    const bool past = li < sel_count && clampi(ids[li], 0, Nb - 1) * a.bk > abs_last;
-    const uint64_t m = __ballot(past);
-    if (m != 0ull) {
-      li_end = base + static_cast<int>(__builtin_ctzll(m));
-      break;
+  {
+    const uint64_t m0 = __ballot(lane < sel_count && id_lane * a.bk > abs_last);
+    if (m0 != 0ull) {
+      li_end = static_cast<int>(__builtin_ctzll(m0));
+    } else {
+      for (int base = 64; base < sel_count; base += 256) {
+        bool found = false;
+        int idv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int li = base + 64 * j + lane;
+          idv[j] = li < sel_count ? clampi(ids[li], 0, Nb - 1) : 0;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int li = base + 64 * j + lane;
+          const uint64_t m = __ballot(li < sel_count && idv[j] * a.bk > abs_last);
+          if (!found && m != 0ull) {
+            li_end = base + 64 * j + static_cast<int>(__builtin_ctzll(m));
+            found = true;
+          }
+        }
+        if (found) break;
+      }
     }
   }
   // Exact-phase sub-tiles: every sub-tile of the blocks before li_end, the
@@ -301,7 +327,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // start past it (only in non-ascending lists) are skipped as empty.
   int n_sel = 0;
   if (li_end > 0) {
-    const int last_blk = clampi(ids[li_end - 1], 0, Nb - 1);
+    const int last_blk = li_end <= 64 ? __builtin_amdgcn_readlane(id_lane, li_end - 1)
+                                      : clampi(ids[li_end - 1], 0, Nb - 1);
     n_sel = (li_end - 1) * subs + min(subs, (abs_last - last_blk * a.bk) / BN + 1);
   }
   const int n_corr = CORR ? (pr_count + BN - 1) / BN : 0;
@@ -314,22 +341,24 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // is read 64 entries per VGPR and handed to the fill lanes with
   // ds_bpermute.
   int win_base = 0, win_key0 = 0, win_nk = 0;
+  auto window_entry = [&](int it, int blk) {
+    const int li = it / subs;
+    const int sub = it - li * subs;
+    const int key0 = blk * a.bk + sub * BN;
+    const int n = min(min(a.bk - sub * BN, BN), a.Lk - key0);
+    win_key0 = key0;
+    win_nk = (it >= n_sel || key0 > abs_last || n < 0) ? 0 : n;
+  };
   auto load_window = [&](int base) {
     const int it = base + lane;
-    int key0 = 0, nk = 0;
-    if (it < n_sel) {
-      const int li = it / subs;  // < li_end
-      const int sub = it - li * subs;
-      key0 = clampi(ids[li], 0, Nb - 1) * a.bk + sub * BN;
-      const int n = min(min(a.bk - sub * BN, BN), a.Lk - key0);
-      nk = (key0 > abs_last || n < 0) ? 0 : n;
-    }
-    win_key0 = key0;
-    win_nk = nk;
+    const int li = it / subs;  // < li_end when it < n_sel
+    window_entry(it, it < n_sel ? clampi(ids[li], 0, Nb - 1) : 0);
   };
-  load_window(0);
+  // the first window's entries come from id_lane (its steps cover at most
+  // the first 64 entries)
+  window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
   int pids_lanes = 0;
-  if constexpr (CORR) pids_lanes = lane < pr_count ? clampi(pids[lane], 0, Nb - 1) : 0;
+  if constexpr (CORR) pids_lanes = lane < pr_count ? pid_lane : 0;
   int walk_it = 0;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
