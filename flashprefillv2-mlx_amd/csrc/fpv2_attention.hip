@@ -10,17 +10,16 @@
 // MI355X mapping:
 //   * one workgroup = one (KV head, query tile, row chunk); the tile's G*tile_q
 //     packed rows (row = g*tile_q + p) share the block lists, so the G query
-//     heads of a KV head share every K/V load.  A workgroup has WAVES = 8
-//     waves (256 rows, one workgroup per CU) when the packed rows come in
-//     multiples of 256, else 4 waves (128 rows);
+//     heads of a KV head share every K/V load.  A workgroup has 4 waves
+//     (128 rows, two workgroups per CU); D = 256 uses 8 waves for the same
+//     rows, two per 32-row group, each owning half of the head dimension;
 //   * each wave owns 32 query rows; Q lives in VGPRs for the whole walk;
 //   * S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: lane l owns query
 //     row l%32 and 16 of the 32 keys of each key tile, so row max/sum need a
 //     single lane-pair exchange and P feeds the next MFMA without a transpose;
 //   * O^T = V^T . P^T: the rescale by exp2(m_old - m_new) is lane-local;
-//   * K/V sub-tiles (64 keys, 32 for D = 256) stream through a ring of NST
-//     LDS stages filled by buffer_load_dwordx4 ... lds, NST-1 sub-tiles ahead
-//     of the multiply; LDS rows are unpadded with an XOR swizzle of their
+//   * K/V sub-tiles of 32 keys stream through a ring of NST LDS stages filled
+//     by buffer_load_dwordx4 ... lds, NST-2 sub-tiles ahead of the multiply; LDS rows are unpadded with an XOR swizzle of their
 //     16-byte chunks, so K (ds_read_b128) and V (ds_read_b64_tr_b16, which
 //     transposes on the way out) are read without bank conflicts and every
 //     wave issues the same number of fills per stage;
@@ -171,19 +170,18 @@ __device__ __forceinline__ int clampi(int x, int lo, int hi) {
 // c ^ mask(r).  The masks make the 16 rows of a ds_read_b128 quarter-wave hit
 // 16 different 16-byte bank groups, and the 4 rows of a transposing read
 // group 4 different 64-byte bank quarters.
-template <int D, int BN_>
+template <int D>
 struct Geom {
   static constexpr int ROWB = D <= 64 ? 128 : (D <= 128 ? 256 : 512);
   static constexpr int RC = ROWB / 16;     // chunks per LDS row
   static constexpr int DG = D / 8;         // chunks holding data
-  static constexpr int BN = BN_;           // keys per sub-tile (32 or 64)
+  static constexpr int BN = 32;            // keys per sub-tile (one slice)
   static constexpr int TILE = BN * ROWB;   // bytes per K (or V) sub-tile
   static constexpr int STAGE = 2 * TILE;   // K then V
   static constexpr int JT = TILE / 1024;   // fill instructions (64 lanes x 16 B) per sub-tile
   static constexpr int RPI = 64 / RC;      // rows per fill instruction
   static constexpr int KS = D / 16;        // QK^T k-steps
   static constexpr int DT = D / 32;        // O^T row tiles (32 dims)
-  static constexpr int NTK = BN / 32;      // S^T key tiles per sub-tile
   static __device__ __forceinline__ int kmask(int row) {
     return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
   }
@@ -205,10 +203,9 @@ struct Step {
 // dimension: each multiplies its half of Q and K into a partial S, the two
 // partials are summed through LDS, both compute P, and each accumulates its
 // half of O.  This keeps D = 256 at two waves per SIMD within 256 registers.
-template <typename T, int D, bool CORR, int WAVES, int NST, int BNK, int DS = 1>
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
 __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
-  using GM = Geom<D, BNK>;
-  static_assert(BNK == 32 || BNK == 64, "sub-tiles of 32 or 64 keys");
+  using GM = Geom<D>;
   static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0), "D split in halves");
   // asm LDS reads unless a wave's registers do not hold them (D = 256 without
   // the split), where the compiler schedules its LDS reads (see lds_read_b128).
@@ -223,9 +220,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   constexpr int NI = 2 * NIK;             // ... per stage (K then V)
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
   static_assert(NST >= 2 && NI * (NST - 2) <= 63, "vmcnt range");
-  __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE];
-  // DS = 2: each wave's partial S (64 lanes x 16 floats) for its partner
-  __shared__ __align__(16) uint8_t xbuf[DS == 2 ? WAVES * 4096 : 16];
+  // the stage ring, then (DS = 2) each wave's partial S (64 lanes x 16
+  // floats) for its partner
+  __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE + (DS == 2 ? WAVES * 4096 : 0)];
+  uint8_t* const xbuf = smem + NST * GM::STAGE;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -778,8 +776,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   using True = std::integral_constant<bool, true>;
   using False = std::integral_constant<bool, false>;
   int cstage = 0;
-  // One sub-tile.  The pending slice enters in s_buf[P] and leaves in
-  // s_buf[P] (two slices) or s_buf[1-P] (one slice per sub-tile).
+  // One sub-tile (one slice).  The pending slice enters in s_buf[P] and
+  // leaves in s_buf[1-P].
   auto do_step = [&](auto first_c, auto p_c) {
     constexpr bool FIRST = decltype(first_c)::value;
     constexpr int P = decltype(p_c)::value;
@@ -795,33 +793,23 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     const Slice s0 = make_slice(cur, cstage, 0);
     if constexpr (FIRST) process(True{}, False{}, NewB{}, s0);
     else process(True{}, True{}, NewB{}, s0);
-    if constexpr (GM::NTK > 1) {
-      if (cur.nkeys > 32) process(True{}, True{}, PendB{}, make_slice(cur, cstage, 1));
-      else s_buf[P] = s_buf[1 - P];
-    }
     cstage = cstage == NST - 1 ? 0 : cstage + 1;
   };
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
   if (n_steps > 0) {
     do_step(True{}, P0{});  // the first sub-tile has no pending slice
-    if constexpr (GM::NTK > 1) {
-      for (int it = 1; it < n_steps; ++it) do_step(False{}, P0{});
+    // the pending buffer alternates, so two sub-tiles per iteration
+    int it = 1;
+    for (; it + 1 < n_steps; it += 2) {
+      do_step(False{}, P1{});
+      do_step(False{}, P0{});
+    }
+    if (it < n_steps) {
+      do_step(False{}, P1{});
       process(False{}, True{}, P1{}, p_pend);  // pending in s_buf[0]
     } else {
-      // one slice per sub-tile: the pending buffer alternates, so two
-      // sub-tiles per iteration
-      int it = 1;
-      for (; it + 1 < n_steps; it += 2) {
-        do_step(False{}, P1{});
-        do_step(False{}, P0{});
-      }
-      if (it < n_steps) {
-        do_step(False{}, P1{});
-        process(False{}, True{}, P1{}, p_pend);  // pending in s_buf[0]
-      } else {
-        process(False{}, True{}, P0{}, p_pend);  // pending in s_buf[1]
-      }
+      process(False{}, True{}, P0{}, p_pend);  // pending in s_buf[1]
     }
   }
   // No fill may land in LDS after the workgroup ends.
@@ -845,9 +833,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   }
 }
 
-template <typename T, int D, bool CORR, int WAVES, int NST, int BNK, int DS = 1>
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
 int launch_attn(AttnArgs a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, BNK, DS>;
+  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS>;
   constexpr int RW = WAVES / DS * 32;
   a.nchunk = (a.G * a.tq + RW - 1) / RW;
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
@@ -856,19 +844,18 @@ int launch_attn(AttnArgs a, hipStream_t stream) {
   return check_launch("sparse_attention");
 }
 
-// Workgroup shape.  D <= 128: 8 waves (256 rows) over 64-key sub-tiles in a
-// 4-stage ring (128 KiB, one workgroup per CU) when the packed rows of a tile
-// come in multiples of 256; else 4 waves (128 rows) over 32-key sub-tiles in
-// a 4-stage ring (64 KiB, two workgroups per CU).  D = 256: 8 waves for 128
-// rows, two per 32-row group each owning half of D (DS = 2), 32-key
-// sub-tiles, 128 KiB.
+// Workgroup shape, 32-key sub-tiles in a 4-stage ring.  D <= 128: 4 waves
+// (128 rows, 64 KiB, two workgroups per CU), tiles of more packed rows in
+// 128-row chunks.  (An 8-wave shape over 64-key sub-tiles, sharing each fill
+// between 256 rows, was measured no faster at 512-row tiles and up to 17 %
+// slower at 256-row tiles.)  D = 256: 8 waves for 128 rows, two per 32-row
+// group each owning half of D (DS = 2), 160 KiB.
 template <typename T, int D, bool CORR>
 int launch_shape(const AttnArgs& a, hipStream_t s) {
   if constexpr (D <= 128) {
-    if ((static_cast<int64_t>(a.G) * a.tq) % 256 == 0) return launch_attn<T, D, CORR, 8, 4, 64>(a, s);
-    return launch_attn<T, D, CORR, 4, 4, 32>(a, s);
+    return launch_attn<T, D, CORR, 4, 4>(a, s);
   } else {
-    return launch_attn<T, D, CORR, 8, 4, 32, 2>(a, s);
+    return launch_attn<T, D, CORR, 8, 4, 2>(a, s);
   }
 }
 

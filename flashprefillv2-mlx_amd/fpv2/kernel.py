@@ -33,8 +33,8 @@ class TileConfig:
 
     Kept for interface parity: ``sparse_attention`` validates a given tile
     with the reference's rules, and the PackGQA alignment rule uses ``bq``.
-    The gfx950 kernel's own tiling (128 packed rows x 32/64-key sub-tiles,
-    4 waves) is fixed per head dimension.
+    The gfx950 kernel's own tiling (128 packed rows x 32-key sub-tiles; 4
+    waves, 8 for head_dim 256) is fixed per head dimension.
     """
 
     bq: int
