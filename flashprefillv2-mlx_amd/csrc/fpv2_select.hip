@@ -264,18 +264,34 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_mfma_kern
       rg_hi[tid] = hi_p;
     }
     // Stage 128 packed rows of Q (zeros past the tile or the valid length).
-    for (int e = tid; e < kRowsPerPass * (D / 8); e += kThreads) {
-      const int r = e / (D / 8);
-      const int c = e - r * (D / 8);
-      const int64_t pr = rc + r;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (pr < R) {
-        const int64_t g = pr / a.tq;
-        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
-        if (pos < a.Lq)
-          v = load16(qbase + (ti.h * a.G + g) * a.q_hs + pos * a.q_rs + c * 8);
+    // For D <= 128 each thread issues all its loads before the stores, so the
+    // staging costs one memory round trip instead of one per load (D = 256
+    // keeps one load at a time: its registers hold no more across the pass).
+    constexpr int QN = kRowsPerPass * (D / 8) / kThreads;
+    static_assert(kRowsPerPass * (D / 8) % kThreads == 0, "Q staging splits evenly");
+    constexpr int QB = D <= 128 ? QN : 1;
+#pragma unroll 1
+    for (int i0 = 0; i0 < QN; i0 += QB) {
+      u32x4 qst[QB];
+#pragma unroll
+      for (int i = 0; i < QB; ++i) {
+        const int e = tid + (i0 + i) * kThreads;
+        const int r = e / (D / 8);
+        const int c = e - r * (D / 8);
+        const int64_t pr = rc + r;
+        qst[i] = u32x4{0u, 0u, 0u, 0u};
+        if (pr < R) {
+          const int64_t g = pr / a.tq;
+          const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
+          if (pos < a.Lq) qst[i] = load16(qbase + (ti.h * a.G + g) * a.q_hs + pos * a.q_rs + c * 8);
+        }
       }
-      store16(qs + r * LDQ + c * 8, v);
+#pragma unroll
+      for (int i = 0; i < QB; ++i) {
+        const int e = tid + (i0 + i) * kThreads;
+        const int r = e / (D / 8);
+        store16(qs + r * LDQ + (e - r * (D / 8)) * 8, qst[i]);
+      }
     }
     __syncthreads();
     const int64_t rows_here = (R - rc) < kRowsPerPass ? (R - rc) : kRowsPerPass;
