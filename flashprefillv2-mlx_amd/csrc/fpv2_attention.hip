@@ -439,6 +439,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
     } else {  // correction: pooled rows of the pruned blocks
       const int w0 = s.li & 63;  // first entry within pids_lanes
+      // When this step uses up the window, the next 64 entries are fetched
+      // before this step's fills are issued: the wait for them, right after
+      // the load, then covers only the older fills (issued a step earlier),
+      // not the ones below.
+      int next_lanes = pids_lanes;
+      if (((s.li + BN) & 63) == 0) {
+        const int li = s.li + BN + lane;
+        next_lanes = li < pr_count ? clampi(pids[li], 0, Nb - 1) : 0;
+      }
       const int ln = opaque_lane();
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -451,10 +460,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
             i < NIK ? pkr : pvr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
             16, off, 0, 0, 0);
       }
-      if (((s.li + BN) & 63) == 0) {  // window used up: fetch the next 64 entries
-        const int li = s.li + BN + lane;
-        pids_lanes = li < pr_count ? clampi(pids[li], 0, Nb - 1) : 0;
-      }
+      pids_lanes = next_lanes;
     }
   };
   // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
