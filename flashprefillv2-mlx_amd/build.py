@@ -67,11 +67,12 @@ def _compile(src: str, obj: Path, verbose: bool) -> None:
         print(msgs, flush=True)
 
 
-# Sources whose device assembly must pass check_isa (asm LDS reads).
-CHECKED = ["fpv2_attention.hip"]
+# Sources whose device assembly must pass check_isa (asm LDS reads), with
+# the kernel symbols to check.
+CHECKED = {"fpv2_attention.hip": "sparse_attn_kernel", "fpv2_select.hip": "select_ring_kernel"}
 
 
-def _check_isa(src: str, tmp: Path, verbose: bool) -> None:
+def _check_isa(src: str, symbol: str, tmp: Path, verbose: bool) -> None:
     """Compile `src` to gfx950 assembly and run the async-LDS-read check."""
     asm = tmp / (Path(src).stem + ".s")
     cmd = [hipcc(), *compile_flags(), "--cuda-device-only", "-S", str(CSRC / src), "-o", str(asm)]
@@ -83,7 +84,7 @@ def _check_isa(src: str, tmp: Path, verbose: bool) -> None:
         import check_isa
     finally:
         sys.path.pop(0)
-    errors = check_isa.check_text(asm.read_text())
+    errors = check_isa.check_text(asm.read_text(), symbol)
     if errors:
         raise RuntimeError(f"{src}: asynchronous LDS read check failed "
                            f"({len(errors)} violations):\n" + "\n".join(errors[:20]))
@@ -96,7 +97,7 @@ def build(jobs: int = 4, verbose: bool = False) -> Path:
     try:
         objs = [tmp / (Path(s).stem + ".o") for s in SOURCES]
         tasks = [lambda so=so: _compile(so[0], so[1], verbose) for so in zip(SOURCES, objs)]
-        tasks += [lambda src=src: _check_isa(src, tmp, verbose) for src in CHECKED]
+        tasks += [lambda src=src, sym=sym: _check_isa(src, sym, tmp, verbose) for src, sym in CHECKED.items()]
         with ThreadPoolExecutor(max_workers=max(1, jobs)) as pool:
             list(pool.map(lambda f: f(), tasks))
         tmp_out = OUT.with_suffix(".so.tmp")

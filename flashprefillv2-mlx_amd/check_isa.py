@@ -1,7 +1,8 @@
-"""Static check of the attention kernels' asynchronous LDS reads.
+"""Static check of the kernels' asynchronous LDS reads.
 
-The sparse-attention kernel issues its LDS reads as inline asm (the compiler
-would otherwise serialise them behind the asynchronous global->LDS fills) and
+The sparse-attention kernel and the ring path of the selection kernel issue
+their LDS reads as inline asm (the compiler would otherwise serialise them
+behind the asynchronous global->LDS fills) and
 waits for them with ``s_waitcnt lgkmcnt(N)``.  The compiler treats the result
 register of such a read as written when the asm statement ends, so nothing
 stops it from copying or spilling that register before the data has arrived.
@@ -13,7 +14,9 @@ still in flight:
   retires all but the N youngest;
 * the text is walked linearly, so instructions on skipped branch paths are
   checked as if executed (conservative), and no read may stay in flight
-  across a backward branch (loop back-edge) or the end of a function;
+  across a backward branch (loop back-edge) or the end of a function (LDS
+  writes, which have no destination registers, still count towards the
+  in-order retirement but may stay in flight);
 * scalar-memory loads also count in lgkmcnt and may complete out of order; a
   wait with N > 0 while such a load is outstanding retires no LDS read.
 
@@ -71,11 +74,11 @@ def check_function(name: str, lines: list[str]) -> list[str]:
         if op in ("s_branch", "s_cbranch_scc0", "s_cbranch_scc1", "s_cbranch_vccz",
                   "s_cbranch_vccnz", "s_cbranch_execz", "s_cbranch_execnz"):
             target = rest.strip()
-            if target in labels and pending:
-                errors.append(f"{name}: LDS read(s) from line(s) {[p[0] for p in pending]} "
+            if target in labels and any(d for _, d in pending):
+                errors.append(f"{name}: LDS read(s) from line(s) {[p[0] for p in pending if p[1]]} "
                               f"in flight across the back-edge at line {i}: {s}")
             continue
-        if op == "s_endpgm" and pending:
+        if op == "s_endpgm" and any(d for _, d in pending):
             errors.append(f"{name}: LDS read(s) in flight at s_endpgm (line {i})")
             continue
         regs = _regs(rest)

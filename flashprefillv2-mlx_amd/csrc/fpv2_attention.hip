@@ -33,36 +33,9 @@
 namespace fpv2 {
 namespace {
 
-// ---- LDS access by inline asm ----
-// Every LDS read of the walk is inline asm.  The compiler cannot tell these
-// reads from the asynchronous global->LDS fills of other stages and would
-// otherwise wait for all outstanding fills before each stage's first read,
-// which serialises the fill latency with the multiply.  Reads complete in
-// order; a read's result is valid after lgkm_wait<N>() (s_waitcnt
-// lgkmcnt(N)) with N no larger than the number of LDS reads issued after it.
-// The wait takes the result registers as operands so that their uses cannot
-// be scheduled before it.  A stage is read only after the fills_done() wait
-// and barrier that completed its fills.
-//
-// With ASM = false (used where register pressure is high enough that the
-// compiler might spill or copy a register between the asm read and its
-// wait) the same reads are ordinary LDS loads and the transposing-read
-// builtin, and the compiler places the waits; the waits below are then
-// no-ops.
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+// ---- LDS access by inline asm (see fpv2_common.h) ----
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-template <bool ASM, int OFF>
-__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
-  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
-  if constexpr (ASM) {
-    u32x4 r;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-    return r;
-  } else {
-    return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr + OFF));
-  }
-}
 // gfx950 transposing read (ds_read_b64_tr_b16): within each 16-lane group
 // lane i receives element i%4 of the 8-byte chunks addressed by lanes
 // i/4, i/4+4, i/4+8, i/4+12.
@@ -79,11 +52,7 @@ __device__ __forceinline__ u32x2 lds_read_tr(uint32_t addr) {
     return __builtin_bit_cast(u32x2, v);
   }
 }
-template <bool ASM, int N>
-__device__ __forceinline__ void lgkm_wait(u32x4& r) {
-  static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
-  if constexpr (ASM) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
-}
+using ::fpv2::lgkm_wait;  // the single-register form, from fpv2_common.h
 template <bool ASM, int N>
 __device__ __forceinline__ void lgkm_wait(u32x2 (&r)[8]) {
   static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
@@ -92,16 +61,6 @@ __device__ __forceinline__ void lgkm_wait(u32x2 (&r)[8]) {
                  : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]),
                    "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
                  : "i"(N));
-}
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
-  // vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
 }
 // In-place multiply; keeps a conditionally rescaled MFMA accumulator in its
 // registers instead of a copy per branch.
@@ -129,17 +88,6 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
-template <int I, int N>
-struct StaticFor {
-  template <typename F>
-  static __device__ __forceinline__ void run(F&& f) {
-    if constexpr (I < N) {
-      f(std::integral_constant<int, I>{});
-      StaticFor<I + 1, N>::run(f);
-    }
-  }
-};
 
 struct AttnArgs {
   const uint16_t* q;

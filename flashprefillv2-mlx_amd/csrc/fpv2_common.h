@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fpv2.h"
 
 namespace fpv2 {
@@ -136,5 +138,62 @@ __device__ __forceinline__ float double_to_float_odd(double x) {
   if (fd != x && __builtin_isfinite(x)) f = __uint_as_float(__float_as_uint(f) | 1u);
   return f;
 }
+
+// ---------------------------------------------------------------------------
+// LDS access by inline asm.  The kernels that stream tiles into LDS with
+// buffer_load ... lds read those tiles by inline asm.  The compiler cannot tell these
+// reads from the asynchronous global->LDS fills of other stages and would
+// otherwise wait for all outstanding fills before each stage's first read,
+// which serialises the fill latency with the multiply.  Reads complete in
+// order; a read's result is valid after lgkm_wait<N>() (s_waitcnt
+// lgkmcnt(N)) with N no larger than the number of LDS reads issued after it.
+// The wait takes the result registers as operands so that their uses cannot
+// be scheduled before it.  A stage is read only after the vmcnt wait and
+// the barrier that completed every wave's fills of it.
+//
+// With ASM = false (used where register pressure is high enough that the
+// compiler might spill or copy a register between the asm read and its
+// wait) the same reads are ordinary LDS loads and the transposing-read
+// builtin, and the compiler places the waits; the waits below are then
+// no-ops.
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+template <bool ASM, int OFF>
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field is 16 bits");
+  if constexpr (ASM) {
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+    return r;
+  } else {
+    return *reinterpret_cast<const lds_u32x4*>(static_cast<uintptr_t>(addr + OFF));
+  }
+}
+template <bool ASM, int N>
+__device__ __forceinline__ void lgkm_wait(u32x4& r) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt is 4 bits");
+  if constexpr (ASM) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(r) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  // vmcnt(N) expcnt(7) lgkmcnt(15): vmcnt bits [3:0] and [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [0, N).
+template <int I, int N>
+struct StaticFor {
+  template <typename F>
+  static __device__ __forceinline__ void run(F&& f) {
+    if constexpr (I < N) {
+      f(std::integral_constant<int, I>{});
+      StaticFor<I + 1, N>::run(f);
+    }
+  }
+};
 
 }  // namespace fpv2

@@ -409,6 +409,250 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_mfma_kern
 }
 
 // ---------------------------------------------------------------------------
+// Ring path: bf16 / f16, head_dim D (multiple of 16), positive scale, no
+// score output -- the hook's path.  Wave w owns the 32 packed rows
+// [32w, 32w + 32) of each 128-row pass, its Q fragments in VGPRs.  The pooled
+// keys stream through an LDS ring of 32-block chunks filled by
+// buffer_load_dwordx4 ... lds kAhead chunks ahead, so the workgroup reads each
+// chunk from L2 once and no wave waits on a global load in the loop.  Every
+// wave multiplies every chunk (S = Q . Kbar^T, a lane holds 16 rows of one
+// block) and reduces its rows to per-block (max, sum) partials; the four
+// waves' partials of a chunk are merged into (c_b, e_b) one chunk later by
+// one wave, through a double-buffered LDS slot.
+// LDS (dynamic only, so that the ring starts at LDS address 0 and its rows
+// are aligned for the XOR-swizzled reads): ring [kRing][32][ROWB] (reused
+// for the flag arrays), c_b[Nb], e_b[Nb], partials [2][4][32] x (c, e),
+// row positions [128], reduction scratch.
+// ---------------------------------------------------------------------------
+template <int D>
+struct RingGeom {
+  static constexpr int ROWB = D <= 64 ? 128 : (D <= 128 ? 256 : 512);  // LDS row (power of two)
+  static constexpr int RC = ROWB / 16;      // 16-byte chunks per LDS row
+  static constexpr int DG = D / 8;          // chunks holding data
+  static constexpr int TILE = 32 * ROWB;    // one 32-block chunk
+  static constexpr int NF = TILE / 1024 / (kThreads / 64);  // fill instructions per wave per chunk
+  static_assert(TILE % (1024 * (kThreads / 64)) == 0, "fills split evenly over the waves");
+  // 16-byte chunk c of row r is stored at chunk c ^ kmask(r): the 16 rows of
+  // a ds_read_b128 quarter-wave then hit 16 different 16-byte bank groups
+  static __device__ __forceinline__ int kmask(int row) {
+    return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
+  }
+};
+constexpr int kAhead = 2;           // chunks filled ahead of the multiply
+constexpr int kRing = kAhead + 1;   // ring stages
+
+template <int D>
+constexpr size_t ring_lds_bytes(int64_t Nb) {
+  return (static_cast<size_t>(kRing) * RingGeom<D>::TILE > static_cast<size_t>(Nb) * 2
+              ? static_cast<size_t>(kRing) * RingGeom<D>::TILE
+              : static_cast<size_t>(Nb) * 2) +
+         static_cast<size_t>(Nb) * 8 + 2 * 4 * 32 * 8 + kRowsPerPass * 4 + 16 + 32;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kernel(SelectArgs a) {
+  using GM = RingGeom<D>;
+  using vec8 = typename Elem<T>::vec8;
+  constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
+  extern __shared__ __align__(1024) unsigned char smem[];
+  constexpr size_t kRingBytes = static_cast<size_t>(kRing) * GM::TILE;
+  const size_t flag_bytes = static_cast<size_t>(a.Nb) * 2;
+  float* cb = reinterpret_cast<float*>(smem + (kRingBytes > flag_bytes ? kRingBytes : flag_bytes));
+  float* eb = cb + a.Nb;
+  float* xpart = eb + a.Nb;  // [2 slots][4 waves][32 blocks] c, then the same for e
+  int* rpos = reinterpret_cast<int*>(xpart + 512);  // local query position, -1: no such row
+  float* fred = reinterpret_cast<float*>(rpos + kRowsPerPass);
+  int* ired = reinterpret_cast<int*>(fred + 4);
+
+  const TileInfo ti = tile_info(a);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hf = lane >> 5;
+  const int64_t R = a.G * a.tq;
+  const int nfv = static_cast<int>(ti.nfv);
+  const int nchunks = (nfv + 31) / 32;
+  const float sc2 = a.scale * kLog2e;  // > 0 on this path
+  const int lq = static_cast<int>(a.Lq);
+
+  for (int b = tid; b < nfv; b += kThreads) {
+    cb[b] = neg_inf();
+    eb[b] = 0.f;
+  }
+
+  // ---- fills: chunk c of the pooled keys into ring stage c % kRing ----
+  // Fill instruction i of this wave covers LDS bytes [1024 j, 1024 (j + 1))
+  // of the stage, j = wave + 4 i: lane -> row (64 j + lane) / RC, stored
+  // chunk p = (64 j + lane) % RC, holding data chunk p ^ kmask(row).  Blocks
+  // past nfv and pad chunks past D load zeros.
+  const rsrc_t pkr = make_rsrc(static_cast<const uint16_t*>(a.pk) + ti.h * a.pk_hs,
+                               static_cast<uint32_t>(a.Nb * D * 2));
+  int fill_off[GM::NF];  // byte offset within the chunk's 32 rows (-1: pad)
+  int fill_row[GM::NF];
+#pragma unroll
+  for (int i = 0; i < GM::NF; ++i) {
+    const int e = 64 * (wave + 4 * i) + lane;
+    const int row = e / GM::RC;
+    const int c = (e % GM::RC) ^ GM::kmask(row);
+    fill_row[i] = row;
+    fill_off[i] = c < GM::DG ? (row * D + c * 8) * 2 : -1;
+  }
+  const uint32_t ring_lds = lds_addr(smem);
+  auto fill_chunk = [&](int c) {
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    uint8_t* const sp = smem + (c % kRing) * GM::TILE;
+#pragma unroll
+    for (int i = 0; i < GM::NF; ++i) {
+      const bool ok = c < nchunks && c * 32 + fill_row[i] < nfv && fill_off[i] >= 0;
+      const uint32_t off = ok ? static_cast<uint32_t>(c * 32 * D * 2 + fill_off[i]) : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(sp + (wave + 4 * i) * 1024), 16, off, 0, 0, 0);
+    }
+  };
+  // K fragment k of the lane's block row l32 (data chunk 2k + hf)
+  const uint32_t kread = (ring_lds + l32 * GM::ROWB + ((16 * hf) ^ (16 * GM::kmask(l32))));
+
+  // merge the four waves' partials of chunk c (slot c & 1) into c_b / e_b
+  // (one common max, then five independent terms)
+  auto merge_chunk = [&](int c) {
+    if (lane < 32 && wave == (c & 3)) {
+      const int b = c * 32 + lane;
+      if (b < nfv) {
+        const float* xc = xpart + (c & 1) * 128 + lane;
+        const float* xe = xpart + 256 + (c & 1) * 128 + lane;
+        float cv[5] = {cb[b], xc[0], xc[32], xc[64], xc[96]};
+        float ev[5] = {eb[b], xe[0], xe[32], xe[64], xe[96]};
+        float m = cv[0];
+#pragma unroll
+        for (int i = 1; i < 5; ++i) m = fmaxf(m, cv[i]);
+        if (m != neg_inf()) {
+          float e = 0.f;
+#pragma unroll
+          for (int i = 0; i < 5; ++i) e += (cv[i] == neg_inf()) ? 0.f : ev[i] * exp2_fast(cv[i] - m);
+          cb[b] = m;
+          eb[b] = e;
+        }
+      }
+    }
+  };
+
+  for (int64_t rc = 0; rc < R; rc += kRowsPerPass) {
+    __syncthreads();  // the previous pass is done with the ring and rpos
+    if (tid < kRowsPerPass) {
+      const int64_t pr = rc + tid;
+      int p = -1;
+      if (pr < R) {
+        const int64_t gg = pr / a.tq;
+        p = static_cast<int>(ti.t * a.tq + (pr - gg * a.tq));
+      }
+      rpos[tid] = p;
+    }
+    // this wave's Q fragments: row rc + 32 wave + l32, data chunks 2k + hf
+    vec8 qf[KS];
+    int my_pos = -1;
+    {
+      const int64_t pr = rc + wave * 32 + l32;
+      const uint16_t* qrow = nullptr;
+      if (pr < R) {
+        const int64_t g = pr / a.tq;
+        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
+        my_pos = static_cast<int>(pos);
+        if (pos < a.Lq) qrow = static_cast<const uint16_t*>(a.q) + (ti.h * a.G + g) * a.q_hs + pos * a.q_rs;
+      }
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        qf[k] = as_vec8<T>(qrow ? load16(qrow + k * 16 + hf * 8) : u32x4{0u, 0u, 0u, 0u});
+    }
+    // lowest / highest position of the wave's rows (-1 rows force the checked path)
+    int g_lo = my_pos, g_hi = my_pos;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) {
+      g_lo = min(g_lo, __shfl_xor(g_lo, o));
+      g_hi = max(g_hi, __shfl_xor(g_hi, o));
+    }
+#pragma unroll
+    for (int c = 0; c < kAhead; ++c) fill_chunk(c);
+
+    for (int c = 0; c < nchunks; ++c) {
+      vm_wait<GM::NF * (kAhead - 1)>();
+      __syncthreads();  // chunk c in LDS; chunk c-1's stage and partial slot are free
+      fill_chunk(c + kAhead);
+      // S = Q . Kbar^T over the chunk: 8 reads in flight, MFMA k after read k
+      const uint32_t ka = kread + (c % kRing) * GM::TILE;
+      u32x4 kf[KS];
+      StaticFor<0, KS>::run([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        kf[k] = lds_read_b128<true, 0>(ka ^ (32 * k));
+      });
+      f32x16 acc = {};
+      StaticFor<0, KS>::run([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        constexpr int younger = KS - 1 - k < 15 ? KS - 1 - k : 15;
+        lgkm_wait<true, younger>(kf[k]);
+        acc = Elem<T>::mfma32(qf[k], as_vec8<T>(kf[k]), acc);
+      });
+      // the previous chunk's merge runs while the MFMAs are in flight
+      if (c > 0) merge_chunk(c - 1);
+      // Lane holds rows (j/4)*8 + hf*4 + j%4 of the wave's 32 rows, block b.
+      const int b = c * 32 + l32;
+      const bool b_scored = b < nfv;
+      const int lo = static_cast<int>(max<int64_t>(0, static_cast<int64_t>(b) * a.bk - a.offset));
+      float cmax = neg_inf(), esum = 0.f;
+      if (__ballot(!(b_scored && g_lo >= lo && g_hi < lq)) == 0ull) {
+        // every row sees the block: no per-row tests
+        float mx = acc[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
+        cmax = mx * sc2;
+        float e0 = 0.f, e1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 16; j += 2) {
+          e0 += exp2_fast(fmaf(acc[j], sc2, -cmax));
+          e1 += exp2_fast(fmaf(acc[j + 1], sc2, -cmax));
+        }
+        esum = e0 + e1;
+      } else {
+        float sv[16];
+        bool ok[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int pos = rpos[wave * 32 + (j >> 2) * 8 + hf * 4 + (j & 3)];
+          sv[j] = acc[j] * sc2;
+          ok[j] = b_scored && pos >= lo && pos < lq;
+          if (ok[j]) cmax = fmaxf(cmax, sv[j]);
+        }
+        if (cmax != neg_inf()) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            if (ok[j]) esum += exp2_fast(sv[j] - cmax);
+        }
+      }
+      // partner lane (hf ^ 1) holds the other 16 rows: one v_permlane32_swap
+      // per value hands each lane both halves
+      {
+        const auto cs = __builtin_amdgcn_permlane32_swap(__float_as_uint(cmax), __float_as_uint(cmax), false, false);
+        const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(esum), __float_as_uint(esum), false, false);
+        cmax = __uint_as_float(cs[0]);
+        esum = __uint_as_float(es[0]);
+        merge_ce(cmax, esum, __uint_as_float(cs[1]), __uint_as_float(es[1]));
+      }
+      if (hf == 0) {
+        xpart[(c & 1) * 128 + wave * 32 + l32] = cmax;
+        xpart[256 + (c & 1) * 128 + wave * 32 + l32] = esum;
+      }
+    }
+    vm_wait<0>();  // the fills past the last chunk
+    __syncthreads();
+    if (nchunks > 0) merge_chunk(nchunks - 1);
+  }
+  __syncthreads();
+  // The ring is free now: reuse it for the flag arrays.
+  uint8_t* fsel = smem;
+  uint8_t* fpr = fsel + a.Nb;
+  finish_tile(a, ti, cb, eb, fsel, fpr, fred, ired);
+}
+
+// ---------------------------------------------------------------------------
 // Generic path (float32 inputs, or head dims without an MFMA instantiation).
 // LDS: Q pass [32][D] float, c_b[Nb], e_b[Nb], flags[2*Nb].
 // ---------------------------------------------------------------------------
@@ -542,6 +786,15 @@ int launch_generic(K kernel, dim3 grid, size_t lds, hipStream_t stream, const Se
 template <typename T>
 int dispatch_mfma(int64_t D, dim3 grid, hipStream_t stream, const SelectArgs& a, bool* done) {
   *done = true;
+  if (a.scores == nullptr && a.scale > 0.f) {
+    switch (D) {
+      case 64: return launch_with_lds(select_ring_kernel<T, 64>, grid, ring_lds_bytes<64>(a.Nb), stream, a);
+      case 96: return launch_with_lds(select_ring_kernel<T, 96>, grid, ring_lds_bytes<96>(a.Nb), stream, a);
+      case 128: return launch_with_lds(select_ring_kernel<T, 128>, grid, ring_lds_bytes<128>(a.Nb), stream, a);
+      case 256: return launch_with_lds(select_ring_kernel<T, 256>, grid, ring_lds_bytes<256>(a.Nb), stream, a);
+      default: break;
+    }
+  }
   const size_t tail = static_cast<size_t>(a.Nb) * 8;
   switch (D) {
     case 64: return launch_with_lds(select_mfma_kernel<T, 64>, grid, 128 * 72 * 2 + tail, stream, a);

@@ -77,3 +77,15 @@ def test_other_functions_are_ignored():
     text = ("other_kernel:\n\tds_read_b128 v[80:83], v84\n\tv_mov_b32_e32 v1, v81\n"
             "\ts_endpgm\n.Lfunc_end0:\n")
     assert check_isa.check_text(text) == []
+
+
+def test_lds_write_may_stay_in_flight_across_back_edge():
+    # a write has no destination registers: only reads must be waited for
+    # before a back-edge; the write still counts in the in-order retirement
+    ok = _fn(".LBB0_1:\n\tds_write_b32 v3, v4\n\ts_cbranch_scc1 .LBB0_1\n")
+    bad = _fn(".LBB0_1:\n\tds_write_b32 v3, v4\n\tds_read_b32 v5, v3\n\ts_cbranch_scc1 .LBB0_1\n")
+    assert check_isa.check_text(ok) == []
+    assert any("back-edge" in e for e in check_isa.check_text(bad))
+    counted = _fn("\tds_read_b128 v[80:83], v84\n\tds_write_b32 v3, v4\n\ts_waitcnt lgkmcnt(1)\n"
+                  "\tv_mov_b32_e32 v1, v81\n")
+    assert check_isa.check_text(counted) == []
