@@ -559,13 +559,12 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // VALU) or in its fills, which keeps the matrix pipe fed (measured: 4%
     // on the 128k layer).
     __builtin_amdgcn_s_setprio(0);
-    // V^T batch 0 of the pending slice, then a window of KW K fragments of
-    // the new one; each QK MFMA issues the read KW fragments ahead.  Reads
+    // A window of KW K fragments of the new slice, then V^T batch 0 of the
+    // pending slice; each QK MFMA issues the read KW fragments ahead.  Reads
     // complete in order, so fragment i is ready once at most the reads issued
-    // after it, min(KW-1, KS-1-i), are outstanding.  The exp section of the
+    // after it are outstanding.  The exp section of the
     // pending slice is spread over the QK MFMAs in source order; an empty asm
     // that consumes each piece keeps the compiler from regrouping them.
-    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
     if constexpr (HN) {
       StaticFor<0, KW>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -573,6 +572,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       });
       s_new = f32x16{};
     }
+    // V^T batch 0 after the first K window: those K reads do not wait behind it
+    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
+    constexpr int NV0 = HP ? 2 * PER_BATCH : 0;  // reads of batch 0
     float bias = 0.f;
     if constexpr (HP) {
       bias = bias_of_ref() + (p_pend.corr ? a.shift : 0.f);
@@ -596,7 +598,12 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
       StaticFor<0, KSQ>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        constexpr int younger = (KSQ - 1 - i) < (KW - 1) ? (KSQ - 1 - i) : (KW - 1);
+        // reads issued after K fragment i: the rest of the first window, the
+        // V batch, and the fragments issued by earlier MFMAs of the loop
+        constexpr int LATE = KSQ - KW > 0 ? KSQ - KW : 0;
+        constexpr int Y0 = KW - 1 - i + NV0 + (i < LATE ? i : LATE);
+        constexpr int younger = i < KW ? (Y0 < 15 ? Y0 : 15)
+                                       : ((KSQ - 1 - i) < (KW - 1) ? (KSQ - 1 - i) : (KW - 1));
         lgkm_wait<kAsm, younger>(kf[i]);
         s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
         if constexpr (i + KW < KSQ) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
