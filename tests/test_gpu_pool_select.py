@@ -164,6 +164,37 @@ def test_selection_and_scores_match_oracle(cuda, dtype, head_dim, offset, qlen):
     assert np.all(np.abs(got - scores_o) <= 1e-5 * np.maximum(1.0, np.abs(scores_o)))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+@pytest.mark.parametrize("offset,qlen,tile_q", [(0, 512, 16), (77, 300, 16), (40, 700, 64)])
+def test_ring_selection_matches_oracle(cuda, dtype, head_dim, offset, qlen, tile_q):
+    # Without a score output the selection runs the LDS-ring kernel (row groups
+    # per wave, pooled-key chunks shared through LDS).  tile_q = 64 gives 256
+    # packed rows per tile: two 128-row passes over the ring.
+    config = FPV2Config(block_k=32, tile_q=tile_q, alpha=0.2, sink_tokens=32, window_tokens=64,
+                        last_n_blocks=1, score_chunk_tiles=4)
+    q, k, _ = structured_qkv(length=offset + qlen + 100, query_heads=8, kv_heads=2,
+                             head_dim=head_dim, block_size=32, seed=head_dim + offset + 1,
+                             dtype=dtype)
+    lq_pad = -(-qlen // tile_q) * tile_q
+    qp = torch.zeros((8, lq_pad, head_dim), dtype=dtype)
+    qp[:, :qlen] = q[:, offset:offset + qlen]
+    nb = -(-(offset + lq_pad) // 32)
+    kp = torch.zeros((2, nb * 32, head_dim), dtype=dtype)
+    n = min(k.shape[1], nb * 32)
+    kp[:, :n] = k[:, :n]
+    pk = pool_blocks(kp.to(cuda), 32)
+    pk_orc = orc.pool_blocks(to_np(kp), 32, out_dtype=_DT[dtype])
+    sel, scores = block_scores_and_select(qp.to(cuda), pk, scale=head_dim ** -0.5,
+                                          config=config, offset=offset, query_length=qlen)
+    assert scores is None
+    sel_o, _, ratio = orc.block_scores_and_select(
+        to_np(qp), pk_orc, scale=head_dim ** -0.5, config=_cfg(config), offset=offset,
+        query_length=qlen, return_ratio=True)
+    _assert_selection_parity(to_np(sel), sel_o, ratio, config.alpha)
+    assert to_np(sel).any(axis=-1).all()  # every tile keeps at least one block
+
+
 def test_float32_selection_path_matches_oracle(cuda):
     config = FPV2Config(block_k=16, tile_q=16, alpha=0.3, sink_tokens=0, window_tokens=16)
     q, k, _ = structured_qkv(length=256, query_heads=4, kv_heads=2, head_dim=48,
