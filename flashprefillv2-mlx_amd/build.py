@@ -84,7 +84,12 @@ def _check_isa(src: str, symbol: str, tmp: Path, verbose: bool) -> None:
         import check_isa
     finally:
         sys.path.pop(0)
-    errors = check_isa.check_text(asm.read_text(), symbol)
+    text = asm.read_text()
+    errors = check_isa.check_text(text, symbol)
+    if symbol == "select_ring_kernel":
+        # its XOR-swizzled ring reads assume the ring starts at LDS address 0:
+        # no static LDS in front of the dynamic area
+        errors += check_isa.check_no_static_lds(text, symbol)
     if errors:
         raise RuntimeError(f"{src}: asynchronous LDS read check failed "
                            f"({len(errors)} violations):\n" + "\n".join(errors[:20]))
