@@ -124,6 +124,16 @@ def test_multi_fragment_rows_match_reference(cuda):
     _run_and_check(cuda, q, k, v, config, tile=TileConfig(64, 32, 4))
 
 
+@pytest.mark.parametrize(("group", "tile_q"), [(1, 128), (3, 32), (3, 64), (8, 16), (8, 64)])
+def test_gqa_ratios_and_tile_rows(cuda, group, tile_q):
+    # packed rows G * tile_q from 96 to 512: partial and multiple 128-row chunks
+    # (tile_q stays a multiple of the reference tile's bq, which it validates)
+    config = FPV2Config(alpha=0.1, sink_tokens=128, window_tokens=256, tile_q=tile_q)
+    q, k, v = structured_qkv(length=1536, query_heads=2 * group, kv_heads=2, head_dim=128,
+                             seed=61 + group)
+    _run_and_check(cuda, q, k, v, config)
+
+
 def test_float16_path(cuda):
     config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256)
     q, k, v = structured_qkv(length=1024, query_heads=8, kv_heads=2, head_dim=128, seed=47)
