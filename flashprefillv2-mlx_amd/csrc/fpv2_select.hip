@@ -203,7 +203,10 @@ __device__ void finish_tile(const SelectArgs& a, const TileInfo& ti, float* cb, 
 }
 
 // ---------------------------------------------------------------------------
-// MFMA path: bf16 / f16 queries and pooled keys, head_dim D (multiple of 16).
+// Score-output path: bf16 / f16 queries and pooled keys, head_dim D (multiple
+// of 16), taken when the caller asks for the scores or the scale is not
+// positive (the ring path below serves the rest).  Each wave owns 32-block
+// chunks of pooled keys in VGPRs and loops over the pass's row groups.
 // LDS: Q pass [128][D+8] (reused for the flag arrays), c_b[Nb], e_b[Nb].
 // ---------------------------------------------------------------------------
 template <typename T, int D>
