@@ -21,7 +21,8 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 INCLUDE = ROOT / "include"
 OUT = HERE / "fpv2" / "libfpv2_hip.so"
-SOURCES = ["fpv2_abi.cpp", "fpv2_pool.hip", "fpv2_select.hip", "fpv2_attention.hip"]
+SOURCES = ["fpv2_abi.cpp", "fpv2_pool.hip", "fpv2_select.hip", "fpv2_attention.hip",
+           "fpv2_decoder.hip"]
 ARCH = "gfx950"
 
 

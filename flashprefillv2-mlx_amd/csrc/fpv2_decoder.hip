@@ -1,0 +1,275 @@
+// Decoder-layer operations of the end-to-end prefill harness: residual add +
+// RMSNorm, per-head Q/K RMSNorm + rotary embedding, SwiGLU gate.  They stand
+// in for mlx-lm's fused mx.fast.rms_norm / mx.fast.rope kernels that the
+// reference's end-to-end runs use (README.md:30-46, external dependency).
+//
+// All three are HBM-bound streaming kernels: each element is read once and
+// written once (the norm re-reads its own row, which it has just touched, from
+// cache).  16-byte vector accesses along rows; float32 arithmetic; one
+// rounding to the storage type per stored value.
+#include "fpv2_common.h"
+#include "fpv2_decoder.h"
+
+namespace fpv2 {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormVecs = FPV2_MAX_NORM_COLS / 8 / kNormThreads;  // 16-byte vectors per thread
+
+template <typename T>
+__device__ __forceinline__ float lo_f(uint32_t w) { return Elem<T>::to_float(w & 0xffffu); }
+template <typename T>
+__device__ __forceinline__ float hi_f(uint32_t w) { return Elem<T>::to_float(w >> 16); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+struct NormArgs {
+  uint16_t* x;
+  const uint16_t* delta;
+  const uint16_t* weight;
+  uint16_t* y;
+  int64_t cols;
+  int64_t x_stride, d_stride, y_stride;
+  float eps;
+};
+
+// One workgroup per row.  Thread t owns the 16-byte vectors t, t + 256, ...
+// of the row and keeps them in registers between the two passes.
+template <typename T>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) {
+  __shared__ float partial[kNormThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nvec = static_cast<int>(a.cols / 8);
+  uint16_t* x = a.x + row * a.x_stride;
+  const uint16_t* d = a.delta ? a.delta + row * a.d_stride : nullptr;
+  u32x4 xv[kNormVecs];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormVecs; ++i) {
+    const int c = tid + i * kNormThreads;
+    if (c < nvec) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(x + 8 * c);
+      if (d != nullptr) {
+        const u32x4 dv = *reinterpret_cast<const u32x4*>(d + 8 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          v[j] = pack2<T>(lo_f<T>(v[j]) + lo_f<T>(dv[j]), hi_f<T>(v[j]) + hi_f<T>(dv[j]));
+        *reinterpret_cast<u32x4*>(x + 8 * c) = v;
+      }
+      xv[i] = v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float l = lo_f<T>(v[j]), h = hi_f<T>(v[j]);
+        ss += l * l + h * h;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) partial[tid >> 6] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / 64; ++w) total += partial[w];
+  const float r = rsqrtf(total / static_cast<float>(a.cols) + a.eps);
+  uint16_t* y = a.y + row * a.y_stride;
+#pragma unroll
+  for (int i = 0; i < kNormVecs; ++i) {
+    const int c = tid + i * kNormThreads;
+    if (c < nvec) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(a.weight + 8 * c);
+      u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = pack2<T>(lo_f<T>(xv[i][j]) * r * lo_f<T>(w[j]),
+                        hi_f<T>(xv[i][j]) * r * hi_f<T>(w[j]));
+      *reinterpret_cast<u32x4*>(y + 8 * c) = o;
+    }
+  }
+}
+
+struct RopeArgs {
+  const uint16_t* qkv;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const float* cos;
+  const float* sin;
+  uint16_t* q_out;
+  uint16_t* k_out;
+  int64_t rows;
+  int64_t qkv_stride;
+  int qh, kh, d;
+  float eps;
+};
+
+// One wave per (row, head) of the query and key heads; lane l handles the
+// rotation pairs (j, j + D/2) for j = l, l + 64.  Four waves per workgroup.
+template <typename T>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int heads = a.qh + a.kh;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= a.rows * heads) return;  // whole wave leaves
+  const int64_t row = item / heads;
+  const int h = static_cast<int>(item - row * heads);
+  const int half = a.d / 2;
+  const bool is_q = h < a.qh;
+  const uint16_t* src = a.qkv + row * a.qkv_stride + static_cast<int64_t>(h) * a.d;
+  const uint16_t* w = is_q ? a.qw : a.kw;
+  uint16_t* dst = is_q ? a.q_out + (row * a.qh + h) * a.d
+                       : a.k_out + (row * a.kh + (h - a.qh)) * a.d;
+  const float* cs = a.cos + row * a.d;
+  const float* sn = a.sin + row * a.d;
+  float x1[2] = {0.f, 0.f}, x2[2] = {0.f, 0.f};
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int j = lane + 64 * p;
+    if (j < half) {
+      x1[p] = Elem<T>::to_float(src[j]);
+      x2[p] = Elem<T>::to_float(src[j + half]);
+      ss += x1[p] * x1[p] + x2[p] * x2[p];
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(a.d) + a.eps);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int j = lane + 64 * p;
+    if (j < half) {
+      // the norm's output is stored in T before the rotation reads it
+      const float n1 = Elem<T>::to_float(Elem<T>::from_float(x1[p] * r * Elem<T>::to_float(w[j])));
+      const float n2 =
+          Elem<T>::to_float(Elem<T>::from_float(x2[p] * r * Elem<T>::to_float(w[j + half])));
+      dst[j] = Elem<T>::from_float(n1 * cs[j] - n2 * sn[j]);
+      dst[j + half] = Elem<T>::from_float(n2 * cs[j + half] + n1 * sn[j + half]);
+    }
+  }
+}
+
+struct SiluArgs {
+  const uint16_t* gu;
+  uint16_t* out;
+  int64_t rows, nvec, cols;
+  int64_t in_stride, out_stride;
+};
+
+__device__ __forceinline__ float silu(float g) { return g / (1.f + __expf(-g)); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
+  const int64_t total = a.rows * a.nvec;
+  for (int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t row = t / a.nvec;
+    const int64_t c = t - row * a.nvec;
+    const uint16_t* g = a.gu + row * a.in_stride + 8 * c;
+    const u32x4 gv = *reinterpret_cast<const u32x4*>(g);
+    const u32x4 uv = *reinterpret_cast<const u32x4*>(g + a.cols);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = pack2<T>(silu(lo_f<T>(gv[j])) * lo_f<T>(uv[j]), silu(hi_f<T>(gv[j])) * hi_f<T>(uv[j]));
+    *reinterpret_cast<u32x4*>(a.out + row * a.out_stride + 8 * c) = o;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace fpv2
+
+extern "C" int fpv2_add_rms_norm(void* x, const void* delta, const void* weight, void* y,
+                                 int dtype, int64_t rows, int64_t cols, int64_t x_row_stride,
+                                 int64_t delta_row_stride, int64_t y_row_stride, float eps,
+                                 void* stream) {
+  using namespace fpv2;
+  if (dtype != FPV2_BF16 && dtype != FPV2_F16)
+    return fail(FPV2_ERR_UNSUPPORTED, "fpv2_add_rms_norm: dtype must be bf16 or f16");
+  if (x == nullptr || weight == nullptr || y == nullptr)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: null pointer");
+  if (rows < 0 || cols <= 0 || cols % 8 || cols > FPV2_MAX_NORM_COLS)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: cols must be a positive multiple of 8 "
+                "and at most %d", FPV2_MAX_NORM_COLS);
+  if (x_row_stride < cols || y_row_stride < cols || x_row_stride % 8 || y_row_stride % 8 ||
+      (delta && (delta_row_stride < cols || delta_row_stride % 8)))
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: row strides must be multiples of 8 "
+                "and at least cols");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(y) || (delta && !aligned16(delta)))
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: pointers must be 16-byte aligned");
+  if (rows == 0) return FPV2_OK;
+  if (rows > 0x7fffffff) return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: too many rows");
+  NormArgs a{static_cast<uint16_t*>(x), static_cast<const uint16_t*>(delta),
+             static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), cols,
+             x_row_stride, delta_row_stride, y_row_stride, eps};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FPV2_BF16)
+    hipLaunchKernelGGL(add_rms_norm_kernel<bf16_t>, dim3(rows), dim3(kNormThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(add_rms_norm_kernel<f16_t>, dim3(rows), dim3(kNormThreads), 0, s, a);
+  return check_launch("add_rms_norm_kernel");
+}
+
+extern "C" int fpv2_qk_norm_rope(const void* qkv, const void* q_weight, const void* k_weight,
+                                 const float* cos, const float* sin, void* q_out, void* k_out,
+                                 int dtype, int64_t rows, int64_t query_heads, int64_t kv_heads,
+                                 int64_t head_dim, int64_t qkv_row_stride, float eps,
+                                 void* stream) {
+  using namespace fpv2;
+  if (dtype != FPV2_BF16 && dtype != FPV2_F16)
+    return fail(FPV2_ERR_UNSUPPORTED, "fpv2_qk_norm_rope: dtype must be bf16 or f16");
+  if (!qkv || !q_weight || !k_weight || !cos || !sin || !q_out || !k_out)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: null pointer");
+  if (head_dim <= 0 || head_dim % 2 || head_dim > 256)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: head_dim must be even and at most 256");
+  if (rows < 0 || query_heads <= 0 || kv_heads <= 0 || query_heads + kv_heads > 4096)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: bad rows or head counts");
+  if (qkv_row_stride < (query_heads + kv_heads) * head_dim)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv rows are shorter than the q and k heads");
+  if (rows == 0) return FPV2_OK;
+  const int64_t waves = rows * (query_heads + kv_heads);
+  const int64_t groups = (waves + 3) / 4;
+  if (groups > 0x7fffffff) return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: too many rows");
+  RopeArgs a{static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_weight),
+             static_cast<const uint16_t*>(k_weight), cos, sin, static_cast<uint16_t*>(q_out),
+             static_cast<uint16_t*>(k_out), rows, qkv_row_stride,
+             static_cast<int>(query_heads), static_cast<int>(kv_heads),
+             static_cast<int>(head_dim), eps};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FPV2_BF16)
+    hipLaunchKernelGGL(qk_norm_rope_kernel<bf16_t>, dim3(groups), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_kernel<f16_t>, dim3(groups), dim3(256), 0, s, a);
+  return check_launch("qk_norm_rope_kernel");
+}
+
+extern "C" int fpv2_silu_mul(const void* gate_up, void* out, int dtype, int64_t rows,
+                             int64_t cols, int64_t in_row_stride, int64_t out_row_stride,
+                             void* stream) {
+  using namespace fpv2;
+  if (dtype != FPV2_BF16 && dtype != FPV2_F16)
+    return fail(FPV2_ERR_UNSUPPORTED, "fpv2_silu_mul: dtype must be bf16 or f16");
+  if (!gate_up || !out) return fail(FPV2_ERR_ARGUMENT, "fpv2_silu_mul: null pointer");
+  if (rows < 0 || cols <= 0 || cols % 8 || in_row_stride < 2 * cols || out_row_stride < cols ||
+      in_row_stride % 8 || out_row_stride % 8)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_silu_mul: cols and row strides must be multiples of 8, "
+                "in_row_stride >= 2 cols, out_row_stride >= cols");
+  if (!aligned16(gate_up) || !aligned16(out))
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_silu_mul: pointers must be 16-byte aligned");
+  if (rows == 0) return FPV2_OK;
+  SiluArgs a{static_cast<const uint16_t*>(gate_up), static_cast<uint16_t*>(out), rows, cols / 8,
+             cols, in_row_stride, out_row_stride};
+  const int64_t total = rows * (cols / 8);
+  const int64_t want = (total + 255) / 256;
+  const unsigned grid = static_cast<unsigned>(want < 8192 ? want : 8192);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FPV2_BF16)
+    hipLaunchKernelGGL(silu_mul_kernel<bf16_t>, dim3(grid), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<f16_t>, dim3(grid), dim3(256), 0, s, a);
+  return check_launch("silu_mul_kernel");
+}

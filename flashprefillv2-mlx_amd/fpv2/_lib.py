@@ -1,4 +1,5 @@
-"""ctypes binding of ``libfpv2_hip.so`` (C ABI declared in ``include/fpv2.h``).
+"""ctypes binding of ``libfpv2_hip.so`` (C ABI declared in ``include/fpv2.h`` and
+``include/fpv2_decoder.h``).
 
 The library is built in-tree by ``flashprefillv2-mlx_amd/build.py``.  There is
 no fallback: if the library is missing or a tensor is not on a ROCm device,
@@ -36,6 +37,10 @@ EXPORTED_SYMBOLS = (
     "fpv2_score_select",
     "fpv2_compact_block_indices",
     "fpv2_sparse_attention",
+    # decoder-layer operations of the end-to-end harness (fpv2_decoder.h)
+    "fpv2_add_rms_norm",
+    "fpv2_qk_norm_rope",
+    "fpv2_silu_mul",
 )
 
 
@@ -115,6 +120,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fpv2_sparse_attention.restype = ctypes.c_int
     lib.fpv2_sparse_attention.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32,
                                           ctypes.POINTER(AttnParams), vp]
+    f32 = ctypes.c_float
+    lib.fpv2_add_rms_norm.restype = ctypes.c_int
+    lib.fpv2_add_rms_norm.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]
+    lib.fpv2_qk_norm_rope.restype = ctypes.c_int
+    lib.fpv2_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
+                                      i64, f32, vp]
+    lib.fpv2_silu_mul.restype = ctypes.c_int
+    lib.fpv2_silu_mul.argtypes = [vp, vp, i32, i64, i64, i64, i64, vp]
 
 
 def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:

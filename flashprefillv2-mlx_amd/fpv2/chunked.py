@@ -151,8 +151,12 @@ class ChunkedPrefill:
         return config
 
     def attend(self, q: torch.Tensor, *, scale: float | None = None, marks=None,
-               keep: dict | None = None) -> torch.Tensor:
-        """Attend ``q`` (the last ``L`` positions of the cached prefix)."""
+               keep: dict | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Attend ``q`` (the last ``L`` positions of the cached prefix).
+
+        ``out``: optional ``[Hq, L, D]`` destination with any head and row
+        stride (D contiguous), e.g. a transposed view of an ``[L, Hq * D]``
+        buffer; the result is written there and returned as ``out[None]``."""
         q3 = self._three_d(q, "q")
         if q3.shape[0] != self.query_heads or q3.shape[-1] != self.head_dim:
             raise ValueError("q must be [query_heads, L, head_dim] of the cache's geometry")
@@ -170,13 +174,19 @@ class ChunkedPrefill:
             self._pool_new_blocks(device, lib)
         if q3.stride(-1) != 1:
             q3 = q3.contiguous()
-        out = torch.empty((1, self.query_heads, q3.shape[1], self.head_dim), dtype=self.dtype,
-                          device=device)
+        if out is None:
+            out = torch.empty((self.query_heads, q3.shape[1], self.head_dim), dtype=self.dtype,
+                              device=device)
+        elif (out.shape != (self.query_heads, q3.shape[1], self.head_dim)
+              or out.dtype != self.dtype or out.stride(-1) != 1):
+            raise ValueError("out must be [query_heads, L, head_dim] of q's dtype with a "
+                             "contiguous last dimension")
+        _lib.require_device(out, q3)
         call_scale = self.head_dim ** -0.5 if scale is None else scale
         _select_attend(q3, k3, v3, self.pooled_k[:, :geo.num_blocks],
-                       self.pooled_v[:, :geo.num_blocks], geo, scale=call_scale, out=out[0],
+                       self.pooled_v[:, :geo.num_blocks], geo, scale=call_scale, out=out,
                        marks=marks, keep=keep)
-        return out
+        return out[None]
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **kwargs) -> torch.Tensor:
         """Append the chunk's K/V, then attend its queries."""

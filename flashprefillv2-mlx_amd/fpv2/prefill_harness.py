@@ -13,8 +13,10 @@ stays off torch's batched bf16 attention paths.
 Architecture (Qwen3 as mlx-lm implements it): RMSNorm before attention and
 MLP, per-head RMSNorm of Q and K, rotary embedding (rotate-half, theta 1e6),
 grouped-query attention, SwiGLU MLP, final RMSNorm, tied LM head.  Linear
-layers are plain 2-D GEMMs (``torch.nn.functional.linear``); norms and RoPE
-compute in float32 and store bf16.
+layers are plain 2-D GEMMs (``torch.nn.functional.linear``); the residual add
++ RMSNorm, the per-head Q/K RMSNorm + RoPE and the SwiGLU gate are fused HIP
+kernels of the same library (``include/fpv2_decoder.h``), computing in float32
+and storing bf16.
 """
 
 from __future__ import annotations
@@ -26,6 +28,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from fpv2 import _lib
 from fpv2.chunked import ChunkedPrefill
 from fpv2.selection import FPV2Config
 
@@ -46,9 +49,43 @@ class DecoderShape:
 QWEN3_4B = DecoderShape()
 
 
-def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+def _add_rms_norm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor,
+                  eps: float) -> torch.Tensor:
+    """``x += delta`` in place (when given), then RMSNorm of ``x``'s rows
+    (``fpv2_add_rms_norm``)."""
+    lib = _lib.load()
+    _lib.require_device(x, weight)
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.check(lib.fpv2_add_rms_norm(
+        x.data_ptr(), _lib.ptr(delta), weight.data_ptr(), y.data_ptr(), _lib.dtype_code(x.dtype),
+        x.shape[0], x.shape[1], x.stride(0), delta.stride(0) if delta is not None else 0,
+        y.stride(0), eps, _lib.stream_ptr(x.device)), "fpv2_add_rms_norm")
+    return y
+
+
+def _qk_norm_rope(qkv: torch.Tensor, q_weight, k_weight, cos, sin, shape) -> tuple:
+    """Per-head RMSNorm + RoPE of the q and k heads of fused projection rows
+    (``fpv2_qk_norm_rope``); returns contiguous ``[L, Hq, D]``, ``[L, Hkv, D]``."""
+    lib = _lib.load()
+    L, s = qkv.shape[0], shape
+    q = torch.empty((L, s.query_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty((L, s.kv_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
+    _lib.check(lib.fpv2_qk_norm_rope(
+        qkv.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        q.data_ptr(), k.data_ptr(), _lib.dtype_code(qkv.dtype), L, s.query_heads, s.kv_heads,
+        s.head_dim, qkv.stride(0), s.rms_eps, _lib.stream_ptr(qkv.device)), "fpv2_qk_norm_rope")
+    return q, k
+
+
+def _silu_mul(gate_up: torch.Tensor, cols: int) -> torch.Tensor:
+    """``silu(gate) * up`` of ``gate_up = [gate | up]`` rows (``fpv2_silu_mul``)."""
+    lib = _lib.load()
+    out = torch.empty((gate_up.shape[0], cols), dtype=gate_up.dtype, device=gate_up.device)
+    _lib.check(lib.fpv2_silu_mul(
+        gate_up.data_ptr(), out.data_ptr(), _lib.dtype_code(gate_up.dtype), gate_up.shape[0],
+        cols, gate_up.stride(0), out.stride(0), _lib.stream_ptr(gate_up.device)),
+        "fpv2_silu_mul")
+    return out
 
 
 def rope_tables(shape: DecoderShape, positions: torch.Tensor):
@@ -58,13 +95,6 @@ def rope_tables(shape: DecoderShape, positions: torch.Tensor):
     ang = positions.to(torch.float64)[:, None] * inv[None, :]
     ang = torch.cat([ang, ang], dim=-1)
     return ang.cos().float(), ang.sin().float()
-
-
-def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """x ``[L, H, D]`` (float32) rotated by position."""
-    half = x.shape[-1] // 2
-    rot = torch.cat([-x[..., half:], x[..., :half]], dim=-1)
-    return x * cos[:, None, :] + rot * sin[:, None, :]
 
 
 class RandomDecoder:
@@ -131,26 +161,25 @@ class ChunkedPrefillRunner:
         for cache in self.caches:
             cache.reset()
 
-    def _layer(self, li: int, x: torch.Tensor, cos, sin) -> torch.Tensor:
+    def _layer(self, li: int, x: torch.Tensor, delta: torch.Tensor | None, cos, sin):
+        """One decoder layer.  The residual stream is ``x + delta``: the add is
+        fused into the next RMSNorm.  Returns the new ``(x, delta)``."""
         s, p = self.model.shape, self.model.layers[li]
         L = x.shape[0]
         qd, kd = s.query_heads * s.head_dim, s.kv_heads * s.head_dim
-        h = _rms_norm(x, p["attn_norm"], s.rms_eps)
+        h = _add_rms_norm(x, delta, p["attn_norm"], s.rms_eps)
         qkv = F.linear(h, p["qkv"])
-        q = qkv[:, :qd].view(L, s.query_heads, s.head_dim)
-        k = qkv[:, qd:qd + kd].view(L, s.kv_heads, s.head_dim)
+        q, k = _qk_norm_rope(qkv, p["q_norm"], p["k_norm"], cos, sin, s)
         v = qkv[:, qd + kd:].view(L, s.kv_heads, s.head_dim)
-        q = _apply_rope(_rms_norm(q, p["q_norm"], s.rms_eps).float(), cos, sin).to(x.dtype)
-        k = _apply_rope(_rms_norm(k, p["k_norm"], s.rms_eps).float(), cos, sin).to(x.dtype)
-        # [L, H, D] -> [H, L, D] views; the kernels read any head/row stride
-        out = self.caches[li].step(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1),
-                                   scale=s.head_dim ** -0.5)
-        attn = out[0].transpose(0, 1).reshape(L, qd)
-        x = x + F.linear(attn, p["o"])
-        h = _rms_norm(x, p["mlp_norm"], s.rms_eps)
-        gu = F.linear(h, p["gate_up"])
-        gate, up = gu[:, :s.intermediate], gu[:, s.intermediate:]
-        return x + F.linear(F.silu(gate) * up, p["down"])
+        # [L, H, D] -> [H, L, D] views; the kernels read and write any
+        # head/row stride, so the attention output lands as [L, Hq * D]
+        attn = torch.empty((L, qd), dtype=x.dtype, device=x.device)
+        self.caches[li].step(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1),
+                             scale=s.head_dim ** -0.5,
+                             out=attn.view(L, s.query_heads, s.head_dim).transpose(0, 1))
+        h = _add_rms_norm(x, F.linear(attn, p["o"]), p["mlp_norm"], s.rms_eps)
+        act = _silu_mul(F.linear(h, p["gate_up"]), s.intermediate)
+        return x, F.linear(act, p["down"])
 
     def prefill(self, tokens: torch.Tensor, chunk: int) -> torch.Tensor:
         """Run the prompt in ``chunk``-token pieces; returns the logits of the
@@ -159,15 +188,15 @@ class ChunkedPrefillRunner:
         n = tokens.numel()
         if n > self.capacity:
             raise ValueError("prompt longer than the KV cache capacity")
-        x = None
+        x = delta = None
         for start in range(0, n, chunk):
             end = min(start + chunk, n)
             pos = torch.arange(start, end, device=m.device)
             cos, sin = rope_tables(m.shape, pos)
-            x = m.embed[tokens[start:end]]
+            x, delta = m.embed[tokens[start:end]], None
             for li in range(m.shape.layers):
-                x = self._layer(li, x, cos, sin)
-        last = _rms_norm(x[-1:], m.final_norm, m.shape.rms_eps)
+                x, delta = self._layer(li, x, delta, cos, sin)
+        last = _add_rms_norm(x[-1:], delta[-1:], m.final_norm, m.shape.rms_eps)
         return F.linear(last, m.embed).float()[0]
 
 

@@ -215,7 +215,7 @@ def test_block_sparsity_starts_at_zero():
 # ---- C ABI -----------------------------------------------------------------
 
 def _declared_symbols() -> set[str]:
-    text = (ROOT / "include" / "fpv2.h").read_text()
+    text = "\n".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     return set(re.findall(r"^\s*(?:int|const char\*)\s+(fpv2_\w+)\s*\(", text, re.M))
 
 
