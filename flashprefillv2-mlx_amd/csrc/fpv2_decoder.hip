@@ -106,47 +106,79 @@ struct RopeArgs {
   float eps;
 };
 
-// One wave per (row, head) of the query and key heads; lane l handles the
-// rotation pairs (j, j + D/2) for j = l, l + 64.  Four waves per workgroup.
+// Sixteen lanes per (row, head) of the query and key heads, four heads per
+// wave: lane s of a group handles the element quads j = 4 (s + 16 p) of the
+// first half and their rotation partners j + D/2 (8-byte loads of the
+// head, 16-byte loads of the float32 tables).
 template <typename T>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
-  const int lane = threadIdx.x & 63;
+  const int sub = threadIdx.x & 15;
   const int heads = a.qh + a.kh;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= a.rows * heads) return;  // whole wave leaves
-  const int64_t row = item / heads;
-  const int h = static_cast<int>(item - row * heads);
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  const bool valid = item < a.rows * heads;  // a group past the end computes nothing
+  const int64_t row = valid ? item / heads : 0;
+  const int h = valid ? static_cast<int>(item - row * heads) : 0;
   const int half = a.d / 2;
+  const int quads = half / 4;
   const bool is_q = h < a.qh;
   const uint16_t* src = a.qkv + row * a.qkv_stride + static_cast<int64_t>(h) * a.d;
   const uint16_t* w = is_q ? a.qw : a.kw;
   uint16_t* dst = is_q ? a.q_out + (row * a.qh + h) * a.d
                        : a.k_out + (row * a.kh + (h - a.qh)) * a.d;
-  const float* cs = a.cos + row * a.d;
-  const float* sn = a.sin + row * a.d;
-  float x1[2] = {0.f, 0.f}, x2[2] = {0.f, 0.f};
+  u32x2 x1[2] = {}, x2[2] = {};
   float ss = 0.f;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const int j = lane + 64 * p;
-    if (j < half) {
-      x1[p] = Elem<T>::to_float(src[j]);
-      x2[p] = Elem<T>::to_float(src[j + half]);
-      ss += x1[p] * x1[p] + x2[p] * x2[p];
+    const int qd = sub + 16 * p;
+    if (valid && qd < quads) {
+      x1[p] = *reinterpret_cast<const u32x2*>(src + 4 * qd);
+      x2[p] = *reinterpret_cast<const u32x2*>(src + 4 * qd + half);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float a1 = lo_f<T>(x1[p][j]), b1 = hi_f<T>(x1[p][j]);
+        const float a2 = lo_f<T>(x2[p][j]), b2 = hi_f<T>(x2[p][j]);
+        ss += a1 * a1 + b1 * b1 + a2 * a2 + b2 * b2;
+      }
     }
   }
-  ss = wave_sum(ss);
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
   const float r = rsqrtf(ss / static_cast<float>(a.d) + a.eps);
+  const float* cs = a.cos + row * a.d;
+  const float* sn = a.sin + row * a.d;
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const int j = lane + 64 * p;
-    if (j < half) {
-      // the norm's output is stored in T before the rotation reads it
-      const float n1 = Elem<T>::to_float(Elem<T>::from_float(x1[p] * r * Elem<T>::to_float(w[j])));
-      const float n2 =
-          Elem<T>::to_float(Elem<T>::from_float(x2[p] * r * Elem<T>::to_float(w[j + half])));
-      dst[j] = Elem<T>::from_float(n1 * cs[j] - n2 * sn[j]);
-      dst[j + half] = Elem<T>::from_float(n2 * cs[j + half] + n1 * sn[j + half]);
+    const int qd = sub + 16 * p;
+    if (valid && qd < quads) {
+      const int j0 = 4 * qd;
+      const u32x2 w1 = *reinterpret_cast<const u32x2*>(w + j0);
+      const u32x2 w2 = *reinterpret_cast<const u32x2*>(w + j0 + half);
+      const f32x4 c1 = *reinterpret_cast<const f32x4*>(cs + j0);
+      const f32x4 c2 = *reinterpret_cast<const f32x4*>(cs + j0 + half);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(sn + j0);
+      const f32x4 s2 = *reinterpret_cast<const f32x4*>(sn + j0 + half);
+      float n1[4], n2[4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        // the norm's output is stored in T before the rotation reads it
+        const uint32_t m1 = pack2<T>(lo_f<T>(x1[p][j]) * r * lo_f<T>(w1[j]),
+                                     hi_f<T>(x1[p][j]) * r * hi_f<T>(w1[j]));
+        const uint32_t m2 = pack2<T>(lo_f<T>(x2[p][j]) * r * lo_f<T>(w2[j]),
+                                     hi_f<T>(x2[p][j]) * r * hi_f<T>(w2[j]));
+        n1[2 * j] = lo_f<T>(m1);
+        n1[2 * j + 1] = hi_f<T>(m1);
+        n2[2 * j] = lo_f<T>(m2);
+        n2[2 * j + 1] = hi_f<T>(m2);
+      }
+      u32x2 o1, o2;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int e = 2 * j;
+        o1[j] = pack2<T>(n1[e] * c1[e] - n2[e] * s1[e], n1[e + 1] * c1[e + 1] - n2[e + 1] * s1[e + 1]);
+        o2[j] = pack2<T>(n2[e] * c2[e] + n1[e] * s2[e], n2[e + 1] * c2[e + 1] + n1[e + 1] * s2[e + 1]);
+      }
+      *reinterpret_cast<u32x2*>(dst + j0) = o1;
+      *reinterpret_cast<u32x2*>(dst + j0 + half) = o2;
     }
   }
 }
@@ -224,15 +256,22 @@ extern "C" int fpv2_qk_norm_rope(const void* qkv, const void* q_weight, const vo
     return fail(FPV2_ERR_UNSUPPORTED, "fpv2_qk_norm_rope: dtype must be bf16 or f16");
   if (!qkv || !q_weight || !k_weight || !cos || !sin || !q_out || !k_out)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: null pointer");
-  if (head_dim <= 0 || head_dim % 2 || head_dim > 256)
-    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: head_dim must be even and at most 256");
+  if (head_dim <= 0 || head_dim % 8 || head_dim > 256)
+    return fail(FPV2_ERR_ARGUMENT,
+                "fpv2_qk_norm_rope: head_dim must be a multiple of 8 and at most 256");
+  if (qkv_row_stride % 4 || reinterpret_cast<uintptr_t>(qkv) % 8 || !aligned16(cos) ||
+      !aligned16(sin) || reinterpret_cast<uintptr_t>(q_weight) % 8 ||
+      reinterpret_cast<uintptr_t>(k_weight) % 8 || reinterpret_cast<uintptr_t>(q_out) % 8 ||
+      reinterpret_cast<uintptr_t>(k_out) % 8)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv_row_stride must be a multiple of 4; "
+                "qkv, weights and outputs 8-byte aligned, cos and sin 16-byte aligned");
   if (rows < 0 || query_heads <= 0 || kv_heads <= 0 || query_heads + kv_heads > 4096)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: bad rows or head counts");
   if (qkv_row_stride < (query_heads + kv_heads) * head_dim)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv rows are shorter than the q and k heads");
   if (rows == 0) return FPV2_OK;
-  const int64_t waves = rows * (query_heads + kv_heads);
-  const int64_t groups = (waves + 3) / 4;
+  const int64_t items = rows * (query_heads + kv_heads);
+  const int64_t groups = (items + 15) / 16;  // 16 (row, head) items per workgroup
   if (groups > 0x7fffffff) return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: too many rows");
   RopeArgs a{static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_weight),
              static_cast<const uint16_t*>(k_weight), cos, sin, static_cast<uint16_t*>(q_out),

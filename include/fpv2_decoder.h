@@ -12,9 +12,10 @@
  *
  * Conventions as in fpv2.h: device pointers, element strides, a hipStream_t
  * passed as void*, FPV2_BF16 or FPV2_F16 data, return FPV2_OK or a negative
- * fpv2_status with fpv2_last_error() set.  Rows are contiguous; row strides
- * and `cols` must be multiples of 8 elements and the row pointers 16-byte
- * aligned (16-byte vector accesses).
+ * fpv2_status with fpv2_last_error() set.  Rows are contiguous; for
+ * fpv2_add_rms_norm and fpv2_silu_mul, row strides and `cols` must be
+ * multiples of 8 elements and the pointers 16-byte aligned (16-byte vector
+ * accesses).
  */
 #ifndef FPV2_DECODER_H_
 #define FPV2_DECODER_H_
@@ -48,7 +49,9 @@ int fpv2_add_rms_norm(void* x, const void* delta, const void* weight, void* y,
  *   out[j]        = round(n[j] cos[r][j]        - n[j+D/2] sin[r][j])
  *   out[j + D/2]  = round(n[j+D/2] cos[r][j+D/2] + n[j] sin[r][j+D/2])
  * q_out [rows, query_heads, D] and k_out [rows, kv_heads, D] are contiguous;
- * cos / sin are float32 [rows, D] contiguous.  head_dim even, <= 256.
+ * cos / sin are float32 [rows, D] contiguous, 16-byte aligned; head_dim a
+ * multiple of 8, <= 256; qkv_row_stride a multiple of 4; qkv, the weights
+ * and the outputs 8-byte aligned.
  * Counterpart of mlx-lm's q_norm / k_norm followed by nn.RoPE
  * (traditional = false) in the Qwen3 attention.
  */
