@@ -224,6 +224,8 @@ extern "C" int fpv2_add_rms_norm(void* x, const void* delta, const void* weight,
     return fail(FPV2_ERR_UNSUPPORTED, "fpv2_add_rms_norm: dtype must be bf16 or f16");
   if (x == nullptr || weight == nullptr || y == nullptr)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: null pointer");
+  if (y == x || y == delta)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: y must not alias x or delta");
   if (rows < 0 || cols <= 0 || cols % 8 || cols > FPV2_MAX_NORM_COLS)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_add_rms_norm: cols must be a positive multiple of 8 "
                 "and at most %d", FPV2_MAX_NORM_COLS);

@@ -49,12 +49,31 @@ class DecoderShape:
 QWEN3_4B = DecoderShape()
 
 
+def _rows(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    """The decoder kernels take 2-D row-major operands (any row stride)."""
+    if t.ndim != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with contiguous rows")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must have dtype {dtype}")
+
+
+def _vector(t: torch.Tensor, name: str, n: int, dtype: torch.dtype) -> None:
+    if t.ndim != 1 or t.numel() != n or not t.is_contiguous() or t.dtype != dtype:
+        raise ValueError(f"{name} must be a contiguous [{n}] vector of dtype {dtype}")
+
+
 def _add_rms_norm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Tensor,
                   eps: float) -> torch.Tensor:
     """``x += delta`` in place (when given), then RMSNorm of ``x``'s rows
     (``fpv2_add_rms_norm``)."""
     lib = _lib.load()
-    _lib.require_device(x, weight)
+    _rows(x, "x", x.dtype)
+    _vector(weight, "weight", x.shape[1], x.dtype)
+    if delta is not None:
+        _rows(delta, "delta", x.dtype)
+        if delta.shape != x.shape:
+            raise ValueError("delta must have x's shape")
+    _lib.require_device(x, weight, *(() if delta is None else (delta,)))
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     _lib.check(lib.fpv2_add_rms_norm(
         x.data_ptr(), _lib.ptr(delta), weight.data_ptr(), y.data_ptr(), _lib.dtype_code(x.dtype),
@@ -68,6 +87,15 @@ def _qk_norm_rope(qkv: torch.Tensor, q_weight, k_weight, cos, sin, shape) -> tup
     (``fpv2_qk_norm_rope``); returns contiguous ``[L, Hq, D]``, ``[L, Hkv, D]``."""
     lib = _lib.load()
     L, s = qkv.shape[0], shape
+    _rows(qkv, "qkv", qkv.dtype)
+    if qkv.shape[1] < (s.query_heads + s.kv_heads) * s.head_dim:
+        raise ValueError("qkv rows are shorter than the q and k heads")
+    _vector(q_weight, "q_weight", s.head_dim, qkv.dtype)
+    _vector(k_weight, "k_weight", s.head_dim, qkv.dtype)
+    for name, table in (("cos", cos), ("sin", sin)):
+        if table.shape != (L, s.head_dim) or not table.is_contiguous() or table.dtype != torch.float32:
+            raise ValueError(f"{name} must be a contiguous float32 [{L}, {s.head_dim}] table")
+    _lib.require_device(qkv, q_weight, k_weight, cos, sin)
     q = torch.empty((L, s.query_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
     k = torch.empty((L, s.kv_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
     _lib.check(lib.fpv2_qk_norm_rope(
@@ -80,6 +108,10 @@ def _qk_norm_rope(qkv: torch.Tensor, q_weight, k_weight, cos, sin, shape) -> tup
 def _silu_mul(gate_up: torch.Tensor, cols: int) -> torch.Tensor:
     """``silu(gate) * up`` of ``gate_up = [gate | up]`` rows (``fpv2_silu_mul``)."""
     lib = _lib.load()
+    _rows(gate_up, "gate_up", gate_up.dtype)
+    if gate_up.shape[1] < 2 * cols:
+        raise ValueError("gate_up rows must hold 2 * cols elements")
+    _lib.require_device(gate_up)
     out = torch.empty((gate_up.shape[0], cols), dtype=gate_up.dtype, device=gate_up.device)
     _lib.check(lib.fpv2_silu_mul(
         gate_up.data_ptr(), out.data_ptr(), _lib.dtype_code(gate_up.dtype), gate_up.shape[0],

@@ -285,3 +285,33 @@ def test_chunked_prefill_validation_without_a_gpu():
         ChunkedPrefill(8, 2, 128, 64, total_tokens=0, device="cpu")
     with pytest.raises(RuntimeError, match="ROCm"):
         ChunkedPrefill(8, 2, 128, 64, device="cpu")
+
+
+def test_decoder_ops_validate_operands_without_a_gpu():
+    """The harness's decoder-kernel wrappers check shapes, dtypes and layouts
+    before any launch (the C ABI cannot see a non-contiguous last dimension)."""
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libfpv2_hip.so not built")
+    from fpv2.prefill_harness import DecoderShape, _add_rms_norm, _qk_norm_rope, _silu_mul
+    bf = torch.bfloat16
+    with pytest.raises(ValueError, match="contiguous rows"):
+        _add_rms_norm(torch.zeros(16, 8, dtype=bf).t(), None, torch.ones(8, dtype=bf), 1e-6)
+    with pytest.raises(ValueError, match="weight"):
+        _add_rms_norm(torch.zeros(4, 16, dtype=bf), None, torch.ones(8, dtype=bf), 1e-6)
+    with pytest.raises(ValueError, match="delta"):
+        _add_rms_norm(torch.zeros(4, 16, dtype=bf), torch.zeros(4, 16), torch.ones(16, dtype=bf),
+                      1e-6)
+    shape = DecoderShape(query_heads=2, kv_heads=1, head_dim=64)
+    w = torch.ones(64, dtype=bf)
+    with pytest.raises(ValueError, match="cos"):
+        _qk_norm_rope(torch.zeros(4, 256, dtype=bf), w, w, torch.zeros(4, 64, dtype=bf),
+                      torch.zeros(4, 64), shape)
+    with pytest.raises(ValueError, match="2 \\* cols"):
+        _silu_mul(torch.zeros(4, 16, dtype=bf), 16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        _silu_mul(torch.zeros(4, 32, dtype=bf), 16)
+    lib = _lib.load()
+    x = 4096  # any non-null address: the aliasing check precedes every launch
+    assert lib.fpv2_add_rms_norm(x, None, 8192, x, _lib.BF16, 1, 8, 8, 0, 8, 1e-6,
+                                 None) == _lib.FPV2_ERR_ARGUMENT
+    assert b"alias" in lib.fpv2_last_error()
