@@ -13,6 +13,8 @@ beside it under ``at_32k``.  ``value`` is retained TFLOP/s of the whole layer
 (retained FLOPs / layer time); ``roofline`` is the attention kernel alone,
 timed with HIP events on the stream it runs on.  ``cpu_baseline`` times the
 numpy oracle (selection + attention) on a bounded sample of the same layer.
+``stock_sdpa`` (and ``at_32k.stock_sdpa``) times PyTorch-ROCm's fused flash
+attention op on the same inputs, the stock dense path FPV2 replaces.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -172,6 +174,39 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
         f"  density {res['density']:.4f}  attn {res['retained_tflops_attention']:.1f} TFLOP/s")
     data = (q, k, v, keep, out)
     return res, data
+
+
+def stock_sdpa(torch, data, seq, ms_fpv2, reps=3):
+    """The stock dense path on the same inputs: PyTorch-ROCm's fused flash
+    attention op (exact causal attention; K/V heads expanded to the query
+    heads, which that op requires).  Reported beside FPV2, not as the metric."""
+    q, k, v, _, out = data
+    g = HQ // HKV
+
+    def expand(t):
+        return t[:, None].expand(HKV, g, seq, D).reshape(1, HQ, seq, D)
+
+    ke, ve = expand(k), expand(v)
+    run = lambda: torch.ops.aten._scaled_dot_product_flash_attention(  # noqa: E731
+        q[None], ke, ve, 0.0, is_causal=True, return_debug_mask=False, scale=D ** -0.5)[0]
+    ref = run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    diff = float((ref[0] - out.reshape(ref[0].shape)).abs().max())
+    del ke, ve, ref
+    torch.cuda.empty_cache()
+    res = {"op": "aten._scaled_dot_product_flash_attention (PyTorch-ROCm build)", "seq": seq,
+           "ms": ms, "tflops": dense_flops(seq) / (ms * 1e-3) / 1e12,
+           "fpv2_layer_speedup": ms / ms_fpv2, "max_abs_diff_vs_fpv2": diff}
+    log(f"seq {seq}: stock flash SDPA {ms:.3f} ms ({res['tflops']:.1f} TFLOP/s dense), "
+        f"FPV2 layer {res['fpv2_layer_speedup']:.2f}x faster, max |diff| {diff:.3g}")
+    return res
 
 
 def cpu_baseline(torch, data, seq, alpha, budget_s: float):
@@ -386,7 +421,10 @@ def main(argv=None) -> int:
     primary, data = run_config(torch, args.seq, args.alpha, args.steps, args.warmup)
     extra = {}
     if not args.profile and args.secondary_seq:
-        sec, _ = run_config(torch, args.secondary_seq, args.alpha, args.steps, args.warmup)
+        sec, sec_data = run_config(torch, args.secondary_seq, args.alpha, args.steps,
+                                   args.warmup)
+        sec["stock_sdpa"] = stock_sdpa(torch, sec_data, args.secondary_seq, sec["ms_per_layer"])
+        del sec_data
         extra["at_32k" if args.secondary_seq == 32768 else f"at_{args.secondary_seq}"] = sec
     if args.extended and not args.profile:
         nc, _ = run_config(torch, 32768, args.alpha, args.steps, args.warmup, corr=False)
@@ -405,6 +443,8 @@ def main(argv=None) -> int:
         e2e = measure(QWEN3_4B, tokens=65536, chunk=2048, alpha=args.alpha, device="cuda:0")
         log(f"e2e: {json.dumps(e2e)}")
         extra["e2e_qwen3_4b_64k"] = e2e
+    if not args.profile:
+        extra["stock_sdpa"] = stock_sdpa(torch, data, args.seq, primary["ms_per_layer"])
     cpu = None
     if not args.profile and args.cpu_budget > 0:
         cpu = cpu_baseline(torch, data, args.seq, args.alpha, args.cpu_budget)

@@ -5,10 +5,11 @@ Measurement harness for the reference's end-to-end prefill comparison
 the same decoder architecture with random weights (there is no network for
 checkpoints), a prompt of uniform-random token ids fed in fixed-size chunks,
 and attention either through FPV2 (``ChunkedPrefill`` per layer: incremental
-pooling, selection, block-sparse attention) or dense.  Dense runs the same
-kernels with every visible block selected (``alpha = 0``), which is exact
-causal attention; it keeps the comparison on one attention implementation and
-stays off torch's batched bf16 attention paths.
+pooling, selection, block-sparse attention), dense or stock.  Dense runs the
+same kernels with every visible block selected (``alpha = 0``), which is exact
+causal attention.  Stock (``"sdpa"``) is the platform's own fused attention:
+PyTorch-ROCm's flash SDPA op, called directly so that torch's unfused batched
+bf16 math path is never taken.
 
 Architecture (Qwen3 as mlx-lm implements it): RMSNorm before attention and
 MLP, per-head RMSNorm of Q and K, rotary embedding (rotate-half, theta 1e6),
@@ -164,18 +165,56 @@ class RandomDecoder:
         return n
 
 
+class _StockAttention:
+    """One layer's KV cache attended by torch's fused SDPA kernel (the flash
+    kernel of the PyTorch-ROCm build): the stock dense path that FPV2 replaces.
+
+    The flash op's causal mask is aligned to the last key when there are fewer
+    queries than keys (each chunk's queries are the last positions of the
+    prefix).  It takes as many K/V heads as query heads, so the cache stores
+    every KV head once per query head of its group (each chunk is expanded
+    once, when appended).  Only that op is called: torch's generic SDPA front
+    end could fall back to its unfused math path."""
+
+    def __init__(self, query_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
+                 dtype, device):
+        self.query_heads, self.kv_heads = query_heads, kv_heads
+        self.k = torch.empty((query_heads, capacity, head_dim), dtype=dtype, device=device)
+        self.v = torch.empty_like(self.k)
+        self.capacity, self.length = capacity, 0
+
+    def reset(self) -> None:
+        self.length = 0
+
+    def step(self, q, k, v, *, scale: float, out: torch.Tensor) -> None:
+        """q ``[Hq, L, D]``, k/v ``[Hkv, L, D]``; writes ``out`` ``[Hq, L, D]``."""
+        n, d = k.shape[1], k.shape[2]
+        if self.length + n > self.capacity:
+            raise ValueError("the KV cache capacity is exceeded")
+        g, hk = self.query_heads // self.kv_heads, self.kv_heads
+        a, b = self.length, self.length + n
+        self.k[:, a:b].view(hk, g, n, d).copy_(k[:, None].expand(hk, g, n, d))
+        self.v[:, a:b].view(hk, g, n, d).copy_(v[:, None].expand(hk, g, n, d))
+        self.length = b
+        o = torch.ops.aten._scaled_dot_product_flash_attention(
+            q.contiguous()[None], self.k[None, :, :b], self.v[None, :, :b], 0.0, is_causal=True,
+            return_debug_mask=False, scale=scale)[0]
+        out.copy_(o[0])
+
+
 class ChunkedPrefillRunner:
     """Chunked prefill of one prompt through a ``RandomDecoder``.
 
-    ``attention``: ``"fpv2"`` (FPV2 with ``config``) or ``"dense"`` (same
-    kernels, every visible block).  ``min_tokens`` is the hook's gate: calls
+    ``attention``: ``"fpv2"`` (FPV2 with ``config``), ``"dense"`` (same
+    kernels, every visible block) or ``"sdpa"`` (torch's fused flash SDPA
+    kernel, the stock dense path).  ``min_tokens`` is the hook's gate: calls
     with fewer keys attend densely in both modes.
     """
 
     def __init__(self, model: RandomDecoder, capacity: int, *, attention: str = "fpv2",
                  config: FPV2Config | None = None, min_tokens: int = 4_096):
-        if attention not in ("fpv2", "dense"):
-            raise ValueError("attention must be 'fpv2' or 'dense'")
+        if attention not in ("fpv2", "dense", "sdpa"):
+            raise ValueError("attention must be 'fpv2', 'dense' or 'sdpa'")
         s = model.shape
         base = config if config is not None else FPV2Config()
         if attention == "dense":
@@ -184,6 +223,11 @@ class ChunkedPrefillRunner:
                               last_n_blocks=base.last_n_blocks,
                               mean_correction=base.mean_correction)
         self.model, self.capacity, self.attention = model, capacity, attention
+        if attention == "sdpa":
+            self.caches = [_StockAttention(s.query_heads, s.kv_heads, s.head_dim, capacity,
+                                           dtype=model.dtype, device=model.device)
+                           for _ in range(s.layers)]
+            return
         self.caches = [ChunkedPrefill(s.query_heads, s.kv_heads, s.head_dim, capacity,
                                       dtype=model.dtype, device=model.device, config=base,
                                       total_tokens=capacity, min_tokens=min_tokens)
@@ -233,7 +277,7 @@ class ChunkedPrefillRunner:
 
 
 def measure(shape: DecoderShape, *, tokens: int, chunk: int, alpha: float, device,
-            seed: int = 0, modes=("fpv2", "dense"), reps: int = 1) -> dict:
+            seed: int = 0, modes=("fpv2", "dense", "sdpa"), reps: int = 1) -> dict:
     """Prefill tok/s and time to first token (prefill + first logits) per mode."""
     model = RandomDecoder(shape, device=device, seed=seed)
     gen = torch.Generator(device=model.device).manual_seed(seed + 1)
@@ -261,4 +305,9 @@ def measure(shape: DecoderShape, *, tokens: int, chunk: int, alpha: float, devic
         res["logits_max_abs_diff"] = float((a - b).abs().max())
         res["top1_agree"] = bool(int(a.argmax()) == int(b.argmax()))
         res["speedup"] = res["dense"]["ttft_s"] / res["fpv2"]["ttft_s"]
+    if "fpv2" in logits and "sdpa" in logits:
+        a, b = logits["fpv2"], logits["sdpa"]
+        res["sdpa_logits_max_abs_diff"] = float((a - b).abs().max())
+        res["sdpa_top1_agree"] = bool(int(a.argmax()) == int(b.argmax()))
+        res["speedup_vs_sdpa"] = res["sdpa"]["ttft_s"] / res["fpv2"]["ttft_s"]
     return res

@@ -85,3 +85,39 @@ def test_runner_rejects_bad_arguments(cuda):
     runner = ChunkedPrefillRunner(model, 256)
     with pytest.raises(ValueError, match="capacity"):
         runner.prefill(torch.zeros(512, dtype=torch.long, device=cuda), 256)
+
+
+def test_stock_sdpa_prefill_matches_float32_cpu(cuda):
+    """The stock comparison path (torch's flash SDPA op, chunk queries aligned
+    to the last keys of the prefix) is exact causal attention too."""
+    model = RandomDecoder(SHAPE, device=cuda, seed=3)
+    tokens = torch.randint(0, SHAPE.vocab, (1024,), generator=torch.Generator().manual_seed(4))
+    runner = ChunkedPrefillRunner(model, 1024, attention="sdpa")
+    got = runner.prefill(tokens.to(cuda), 256).cpu()
+    ref = _cpu_forward(model, tokens)[0]
+    rel = float((got - ref).abs().max() / ref.abs().max())
+    assert rel < 3e-2, rel
+
+
+def test_stock_attention_aligns_chunk_queries_to_the_last_keys(cuda):
+    from fpv2.prefill_harness import _StockAttention
+    hq, hk, d = 8, 2, 128
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn((hq, 768, d), generator=g).bfloat16()
+    k = torch.randn((hk, 768, d), generator=g).bfloat16()
+    v = torch.randn((hk, 768, d), generator=g).bfloat16()
+    layer = _StockAttention(hq, hk, d, 768, dtype=torch.bfloat16, device=cuda)
+    out = torch.empty((hq, 256, d), dtype=torch.bfloat16, device=cuda)
+    for start, end in ((0, 512), (512, 768)):
+        o = torch.empty((hq, end - start, d), dtype=torch.bfloat16, device=cuda)
+        layer.step(q[:, start:end].to(cuda), k[:, start:end].to(cuda), v[:, start:end].to(cuda),
+                   scale=d ** -0.5, out=o)
+    out = o.cpu().float()
+    # float32 reference of the second chunk: query i sits at position 512 + i
+    kf = k.float().repeat_interleave(hq // hk, dim=0)
+    vf = v.float().repeat_interleave(hq // hk, dim=0)
+    s = q[:, 512:].float() @ kf.transpose(1, 2) * d ** -0.5
+    pos = torch.arange(512, 768)[:, None]
+    s = s.masked_fill(torch.arange(768)[None, :] > pos, float("-inf"))
+    ref = torch.softmax(s, dim=-1) @ vf
+    assert float((out - ref).abs().max()) < 2e-2
