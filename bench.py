@@ -343,6 +343,25 @@ def run_chunked(torch, total: int, chunk: int, alpha: float):
         f_ret += f
         off = keep["offset"]
         f_dense += 4 * D * HQ * (lq * off + lq * (lq + 1) // 2)
+    # stock dense path on the same chunks: PyTorch-ROCm's flash SDPA op
+    from fpv2.prefill_harness import _StockAttention
+    stock = _StockAttention(HQ, HKV, D, total, dtype=q.dtype, device=dev)
+
+    def stock_pass():
+        stock.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s0 in range(0, total, chunk):
+            s1 = min(s0 + chunk, total)
+            o = torch.empty((HQ, s1 - s0, D), dtype=q.dtype, device=dev)
+            stock.step(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], scale=scale, out=o)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    stock_pass()  # warm-up
+    stock_ms = stock_pass()
+    del stock
+    torch.cuda.empty_cache()
     res = {
         "total_tokens": total,
         "chunk": chunk,
@@ -359,7 +378,11 @@ def run_chunked(torch, total: int, chunk: int, alpha: float):
         "dense_flops": f_dense,
         "density": f_ret / f_dense,
         "retained_tflops_attention": f_ret / (stage["attention"] * 1e-3) / 1e12,
+        "stock_sdpa_ms_total": stock_ms,
+        "speedup_vs_stock_sdpa": stock_ms / wall,
     }
+    log(f"chunked {total}/{chunk}: stock flash SDPA {stock_ms:.1f} ms "
+        f"({res['speedup_vs_stock_sdpa']:.2f}x slower than FPV2)")
     log(f"chunked {total}/{chunk}: {wall:.1f} ms ({res['tok_per_s']:.0f} tok/s), stages "
         f"{json.dumps({k_: round(v_, 3) for k_, v_ in stage.items()})}; hook-style re-pooling "
         f"{wall_re:.1f} ms, pool {stage_re['pool']:.3f} ms")
