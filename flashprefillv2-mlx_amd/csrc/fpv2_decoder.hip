@@ -100,31 +100,36 @@ struct RopeArgs {
   const float* sin;
   uint16_t* q_out;
   uint16_t* k_out;
+  uint16_t* v_out;  // null: no V heads
   int64_t rows;
   int64_t qkv_stride;
+  int64_t q_hs, q_rs;    // q_out head / row strides
+  int64_t kv_hs, kv_rs;  // k_out and v_out head / row strides
   int qh, kh, d;
   float eps;
 };
 
-// Sixteen lanes per (row, head) of the query and key heads, four heads per
-// wave: lane s of a group handles the element quads j = 4 (s + 16 p) of the
-// first half and their rotation partners j + D/2 (8-byte loads of the
+// Sixteen lanes per (row, head) item, four items per wave: the query and key
+// heads are normalised and rotated, the value heads (when v_out is given) are
+// copied.  Lane s of a group handles the element quads j = 4 (s + 16 p) of
+// the first half and their rotation partners j + D/2 (8-byte loads of the
 // head, 16-byte loads of the float32 tables).
 template <typename T>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   const int sub = threadIdx.x & 15;
-  const int heads = a.qh + a.kh;
+  const int heads = a.qh + a.kh + (a.v_out != nullptr ? a.kh : 0);
   const int64_t item = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
   const bool valid = item < a.rows * heads;  // a group past the end computes nothing
   const int64_t row = valid ? item / heads : 0;
   const int h = valid ? static_cast<int>(item - row * heads) : 0;
   const int half = a.d / 2;
   const int quads = half / 4;
-  const bool is_q = h < a.qh;
+  const int kind = h < a.qh ? 0 : (h < a.qh + a.kh ? 1 : 2);  // q, k, v
   const uint16_t* src = a.qkv + row * a.qkv_stride + static_cast<int64_t>(h) * a.d;
-  const uint16_t* w = is_q ? a.qw : a.kw;
-  uint16_t* dst = is_q ? a.q_out + (row * a.qh + h) * a.d
-                       : a.k_out + (row * a.kh + (h - a.qh)) * a.d;
+  const uint16_t* w = kind == 0 ? a.qw : a.kw;
+  uint16_t* dst = kind == 0 ? a.q_out + row * a.q_rs + h * a.q_hs
+                : kind == 1 ? a.k_out + row * a.kv_rs + (h - a.qh) * a.kv_hs
+                            : a.v_out + row * a.kv_rs + (h - a.qh - a.kh) * a.kv_hs;
   u32x2 x1[2] = {}, x2[2] = {};
   float ss = 0.f;
 #pragma unroll
@@ -141,8 +146,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
       }
     }
   }
+  // the four groups of a wave reduce together; each keeps its own sum
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+  if (kind == 2) {  // value head: copy
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int qd = sub + 16 * p;
+      if (valid && qd < quads) {
+        *reinterpret_cast<u32x2*>(dst + 4 * qd) = x1[p];
+        *reinterpret_cast<u32x2*>(dst + 4 * qd + half) = x2[p];
+      }
+    }
+    return;
+  }
   const float r = rsqrtf(ss / static_cast<float>(a.d) + a.eps);
   const float* cs = a.cos + row * a.d;
   const float* sn = a.sin + row * a.d;
@@ -250,10 +267,13 @@ extern "C" int fpv2_add_rms_norm(void* x, const void* delta, const void* weight,
 
 extern "C" int fpv2_qk_norm_rope(const void* qkv, const void* q_weight, const void* k_weight,
                                  const float* cos, const float* sin, void* q_out, void* k_out,
-                                 int dtype, int64_t rows, int64_t query_heads, int64_t kv_heads,
-                                 int64_t head_dim, int64_t qkv_row_stride, float eps,
+                                 void* v_out, int dtype, int64_t rows, int64_t query_heads,
+                                 int64_t kv_heads, int64_t head_dim, int64_t qkv_row_stride,
+                                 int64_t q_head_stride, int64_t q_row_stride,
+                                 int64_t kv_head_stride, int64_t kv_row_stride, float eps,
                                  void* stream) {
   using namespace fpv2;
+  const auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
   if (dtype != FPV2_BF16 && dtype != FPV2_F16)
     return fail(FPV2_ERR_UNSUPPORTED, "fpv2_qk_norm_rope: dtype must be bf16 or f16");
   if (!qkv || !q_weight || !k_weight || !cos || !sin || !q_out || !k_out)
@@ -261,23 +281,28 @@ extern "C" int fpv2_qk_norm_rope(const void* qkv, const void* q_weight, const vo
   if (head_dim <= 0 || head_dim % 8 || head_dim > 256)
     return fail(FPV2_ERR_ARGUMENT,
                 "fpv2_qk_norm_rope: head_dim must be a multiple of 8 and at most 256");
-  if (qkv_row_stride % 4 || reinterpret_cast<uintptr_t>(qkv) % 8 || !aligned16(cos) ||
-      !aligned16(sin) || reinterpret_cast<uintptr_t>(q_weight) % 8 ||
-      reinterpret_cast<uintptr_t>(k_weight) % 8 || reinterpret_cast<uintptr_t>(q_out) % 8 ||
-      reinterpret_cast<uintptr_t>(k_out) % 8)
-    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv_row_stride must be a multiple of 4; "
-                "qkv, weights and outputs 8-byte aligned, cos and sin 16-byte aligned");
-  if (rows < 0 || query_heads <= 0 || kv_heads <= 0 || query_heads + kv_heads > 4096)
+  if (rows < 0 || query_heads <= 0 || kv_heads <= 0 || query_heads + 2 * kv_heads > 4096)
     return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: bad rows or head counts");
-  if (qkv_row_stride < (query_heads + kv_heads) * head_dim)
-    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv rows are shorter than the q and k heads");
+  const int64_t in_heads = query_heads + kv_heads + (v_out ? kv_heads : 0);
+  if (qkv_row_stride < in_heads * head_dim)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv rows are shorter than the heads read");
+  if (qkv_row_stride % 4 || q_head_stride % 4 || q_row_stride % 4 || kv_head_stride % 4 ||
+      kv_row_stride % 4 || q_head_stride < head_dim || kv_head_stride < head_dim ||
+      q_row_stride <= 0 || kv_row_stride <= 0)
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: strides must be positive multiples of 4 "
+                "and head strides at least head_dim");
+  if (!a8(qkv) || !aligned16(cos) || !aligned16(sin) || !a8(q_weight) || !a8(k_weight) ||
+      !a8(q_out) || !a8(k_out) || (v_out && !a8(v_out)))
+    return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: qkv, weights and outputs must be 8-byte "
+                "aligned, cos and sin 16-byte aligned");
   if (rows == 0) return FPV2_OK;
-  const int64_t items = rows * (query_heads + kv_heads);
+  const int64_t items = rows * in_heads;
   const int64_t groups = (items + 15) / 16;  // 16 (row, head) items per workgroup
   if (groups > 0x7fffffff) return fail(FPV2_ERR_ARGUMENT, "fpv2_qk_norm_rope: too many rows");
   RopeArgs a{static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(q_weight),
              static_cast<const uint16_t*>(k_weight), cos, sin, static_cast<uint16_t*>(q_out),
-             static_cast<uint16_t*>(k_out), rows, qkv_row_stride,
+             static_cast<uint16_t*>(k_out), static_cast<uint16_t*>(v_out), rows, qkv_row_stride,
+             q_head_stride, q_row_stride, kv_head_stride, kv_row_stride,
              static_cast<int>(query_heads), static_cast<int>(kv_heads),
              static_cast<int>(head_dim), eps};
   const hipStream_t s = static_cast<hipStream_t>(stream);

@@ -124,8 +124,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fpv2_add_rms_norm.restype = ctypes.c_int
     lib.fpv2_add_rms_norm.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]
     lib.fpv2_qk_norm_rope.restype = ctypes.c_int
-    lib.fpv2_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
-                                      i64, f32, vp]
+    lib.fpv2_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i32, i64, i64, i64, i64,
+                                      i64, i64, i64, i64, i64, f32, vp]
     lib.fpv2_silu_mul.restype = ctypes.c_int
     lib.fpv2_silu_mul.argtypes = [vp, vp, i32, i64, i64, i64, i64, vp]
 

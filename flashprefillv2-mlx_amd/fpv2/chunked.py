@@ -116,12 +116,19 @@ class ChunkedPrefill:
             raise ValueError("k and v must be [kv_heads, L, head_dim] of the cache's geometry")
         if k.dtype != self.dtype or v.dtype != self.dtype:
             raise ValueError("q, k, and v must share float16 or bfloat16 dtype")
-        n = k.shape[1]
-        if self.length + n > self.capacity:
+        k_rows, v_rows = self.reserve(k.shape[1])
+        k_rows.copy_(k)
+        v_rows.copy_(v)
+
+    def reserve(self, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append ``n`` rows without copying: returns the cache's next ``n``
+        rows as ``[kv_heads, n, head_dim]`` views of K and V, for a producer
+        that writes them in place (e.g. the kernel that normalises and
+        rotates K).  They count as appended: fill them before ``attend``."""
+        if n < 0 or self.length + n > self.capacity:
             raise ValueError("the KV cache capacity is exceeded")
-        self.k[:, self.length:self.length + n].copy_(k)
-        self.v[:, self.length:self.length + n].copy_(v)
-        self.length += n
+        a, self.length = self.length, self.length + n
+        return self.k[:, a:self.length], self.v[:, a:self.length]
 
     def _pool_new_blocks(self, device, lib) -> None:
         bk = self.config.block_k

@@ -83,27 +83,45 @@ def _add_rms_norm(x: torch.Tensor, delta: torch.Tensor | None, weight: torch.Ten
     return y
 
 
-def _qk_norm_rope(qkv: torch.Tensor, q_weight, k_weight, cos, sin, shape) -> tuple:
+def _qk_norm_rope(qkv: torch.Tensor, q_weight, k_weight, cos, sin, shape, *,
+                  k_out: torch.Tensor | None = None,
+                  v_out: torch.Tensor | None = None) -> tuple:
     """Per-head RMSNorm + RoPE of the q and k heads of fused projection rows
-    (``fpv2_qk_norm_rope``); returns contiguous ``[L, Hq, D]``, ``[L, Hkv, D]``."""
+    (``fpv2_qk_norm_rope``).  Returns ``q`` ``[Hq, L, D]`` (a view of an
+    ``[L, Hq, D]`` buffer) and ``k`` ``[Hkv, L, D]``, written into ``k_out``
+    when given (any head/row stride, e.g. rows of a KV cache).  ``v_out``
+    (``[Hkv, L, D]``), when given, receives a copy of the value heads."""
     lib = _lib.load()
     L, s = qkv.shape[0], shape
     _rows(qkv, "qkv", qkv.dtype)
-    if qkv.shape[1] < (s.query_heads + s.kv_heads) * s.head_dim:
-        raise ValueError("qkv rows are shorter than the q and k heads")
+    heads = s.query_heads + s.kv_heads * (2 if v_out is not None else 1)
+    if qkv.shape[1] < heads * s.head_dim:
+        raise ValueError("qkv rows are shorter than the heads read")
     _vector(q_weight, "q_weight", s.head_dim, qkv.dtype)
     _vector(k_weight, "k_weight", s.head_dim, qkv.dtype)
     for name, table in (("cos", cos), ("sin", sin)):
         if table.shape != (L, s.head_dim) or not table.is_contiguous() or table.dtype != torch.float32:
             raise ValueError(f"{name} must be a contiguous float32 [{L}, {s.head_dim}] table")
-    _lib.require_device(qkv, q_weight, k_weight, cos, sin)
+    if k_out is None:
+        k_out = torch.empty((L, s.kv_heads, s.head_dim), dtype=qkv.dtype,
+                            device=qkv.device).transpose(0, 1)
+    for name, t in (("k_out", k_out), ("v_out", v_out)):
+        if t is not None and (t.shape != (s.kv_heads, L, s.head_dim) or t.stride(-1) != 1
+                              or t.dtype != qkv.dtype):
+            raise ValueError(f"{name} must be [{s.kv_heads}, {L}, {s.head_dim}] of qkv's dtype "
+                             "with a contiguous last dimension")
+    if v_out is not None and v_out.stride()[:2] != k_out.stride()[:2]:
+        raise ValueError("k_out and v_out must share strides")
+    _lib.require_device(qkv, q_weight, k_weight, cos, sin, k_out,
+                        *(() if v_out is None else (v_out,)))
     q = torch.empty((L, s.query_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
-    k = torch.empty((L, s.kv_heads, s.head_dim), dtype=qkv.dtype, device=qkv.device)
     _lib.check(lib.fpv2_qk_norm_rope(
         qkv.data_ptr(), q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-        q.data_ptr(), k.data_ptr(), _lib.dtype_code(qkv.dtype), L, s.query_heads, s.kv_heads,
-        s.head_dim, qkv.stride(0), s.rms_eps, _lib.stream_ptr(qkv.device)), "fpv2_qk_norm_rope")
-    return q, k
+        q.data_ptr(), k_out.data_ptr(), _lib.ptr(v_out), _lib.dtype_code(qkv.dtype), L,
+        s.query_heads, s.kv_heads, s.head_dim, qkv.stride(0), q.stride(1), q.stride(0),
+        k_out.stride(0), k_out.stride(1), s.rms_eps, _lib.stream_ptr(qkv.device)),
+        "fpv2_qk_norm_rope")
+    return q.transpose(0, 1), k_out
 
 
 def _silu_mul(gate_up: torch.Tensor, cols: int) -> torch.Tensor:
@@ -245,14 +263,21 @@ class ChunkedPrefillRunner:
         qd, kd = s.query_heads * s.head_dim, s.kv_heads * s.head_dim
         h = _add_rms_norm(x, delta, p["attn_norm"], s.rms_eps)
         qkv = F.linear(h, p["qkv"])
-        q, k = _qk_norm_rope(qkv, p["q_norm"], p["k_norm"], cos, sin, s)
-        v = qkv[:, qd + kd:].view(L, s.kv_heads, s.head_dim)
-        # [L, H, D] -> [H, L, D] views; the kernels read and write any
-        # head/row stride, so the attention output lands as [L, Hq * D]
+        cache = self.caches[li]
+        # the attention output lands as [L, Hq * D], the layout the output
+        # projection reads (the kernels write any head/row stride)
         attn = torch.empty((L, qd), dtype=x.dtype, device=x.device)
-        self.caches[li].step(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1),
-                             scale=s.head_dim ** -0.5,
-                             out=attn.view(L, s.query_heads, s.head_dim).transpose(0, 1))
+        attn_heads = attn.view(L, s.query_heads, s.head_dim).transpose(0, 1)
+        if self.attention == "sdpa":
+            q, k = _qk_norm_rope(qkv, p["q_norm"], p["k_norm"], cos, sin, s)
+            v = qkv[:, qd + kd:].view(L, s.kv_heads, s.head_dim).transpose(0, 1)
+            cache.step(q, k, v, scale=s.head_dim ** -0.5, out=attn_heads)
+        else:
+            # K (normalised, rotated) and V go straight into the layer's cache
+            k_rows, v_rows = cache.reserve(L)
+            q, _ = _qk_norm_rope(qkv, p["q_norm"], p["k_norm"], cos, sin, s,
+                                 k_out=k_rows, v_out=v_rows)
+            cache.attend(q, scale=s.head_dim ** -0.5, out=attn_heads)
         h = _add_rms_norm(x, F.linear(attn, p["o"]), p["mlp_norm"], s.rms_eps)
         act = _silu_mul(F.linear(h, p["gate_up"]), s.intermediate)
         return x, F.linear(act, p["down"])

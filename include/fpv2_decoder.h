@@ -44,22 +44,29 @@ int fpv2_add_rms_norm(void* x, const void* delta, const void* weight, void* y,
 
 /*
  * Per-head RMSNorm and rotate-half rotary embedding of the query and key
- * heads of fused projection rows qkv[r] = [q heads | k heads | v heads]:
+ * heads of fused projection rows qkv[r] = [q heads | k heads | v heads],
+ * with the value heads copied alongside:
  *   n = round(x * rsqrt(mean(x^2) + eps) * weight)       (norm output dtype)
  *   out[j]        = round(n[j] cos[r][j]        - n[j+D/2] sin[r][j])
  *   out[j + D/2]  = round(n[j+D/2] cos[r][j+D/2] + n[j] sin[r][j+D/2])
- * q_out [rows, query_heads, D] and k_out [rows, kv_heads, D] are contiguous;
- * cos / sin are float32 [rows, D] contiguous, 16-byte aligned; head_dim a
- * multiple of 8, <= 256; qkv_row_stride a multiple of 4; qkv, the weights
- * and the outputs 8-byte aligned.
+ * Query head h of row r goes to q_out + r*q_row_stride + h*q_head_stride,
+ * key head h to k_out + r*kv_row_stride + h*kv_head_stride, and value head h
+ * (unchanged) to v_out at the same offsets; v_out may be NULL (no copy).
+ * With kv strides of a [kv_heads, capacity, D] cache, K and V land in the
+ * cache directly.  cos / sin are float32 [rows, D] contiguous, 16-byte
+ * aligned; head_dim a multiple of 8, <= 256; every stride a multiple of 4;
+ * qkv, the weights and the outputs 8-byte aligned.
  * Counterpart of mlx-lm's q_norm / k_norm followed by nn.RoPE
- * (traditional = false) in the Qwen3 attention.
+ * (traditional = false) in the Qwen3 attention, and of its KV-cache update.
  */
 int fpv2_qk_norm_rope(const void* qkv, const void* q_weight,
                       const void* k_weight, const float* cos, const float* sin,
-                      void* q_out, void* k_out, int dtype, int64_t rows,
-                      int64_t query_heads, int64_t kv_heads, int64_t head_dim,
-                      int64_t qkv_row_stride, float eps, void* stream);
+                      void* q_out, void* k_out, void* v_out, int dtype,
+                      int64_t rows, int64_t query_heads, int64_t kv_heads,
+                      int64_t head_dim, int64_t qkv_row_stride,
+                      int64_t q_head_stride, int64_t q_row_stride,
+                      int64_t kv_head_stride, int64_t kv_row_stride, float eps,
+                      void* stream);
 
 /*
  * SwiGLU gate: out[r][c] = round(silu(g) * u) with g = gate_up[r][c],

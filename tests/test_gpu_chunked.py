@@ -82,3 +82,26 @@ def test_reset_and_capacity(cuda):
     again = cp.step(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(first, again)
+
+
+def test_reserve_then_fill_equals_append(cuda):
+    """``reserve`` hands out the cache rows ``append`` would copy into."""
+    from fpv2 import ChunkedPrefill
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn((2, 300, 64), generator=g).bfloat16().to(cuda)
+    v = torch.randn((2, 300, 64), generator=g).bfloat16().to(cuda)
+    q = torch.randn((8, 300, 64), generator=g).bfloat16().to(cuda)
+    a = ChunkedPrefill(8, 2, 64, 512, device=cuda, min_tokens=1)
+    b = ChunkedPrefill(8, 2, 64, 512, device=cuda, min_tokens=1)
+    outs = []
+    for s0, s1 in ((0, 200), (200, 300)):
+        a.append(k[:, s0:s1], v[:, s0:s1])
+        kr, vr = b.reserve(s1 - s0)
+        kr.copy_(k[:, s0:s1])
+        vr.copy_(v[:, s0:s1])
+        outs.append((a.attend(q[:, s0:s1]), b.attend(q[:, s0:s1])))
+    torch.cuda.synchronize()
+    for x, y in outs:
+        assert torch.equal(x, y)
+    with pytest.raises(ValueError, match="capacity"):
+        b.reserve(213)

@@ -49,7 +49,8 @@ def test_add_rms_norm(cuda, dtype, rows, cols, with_delta):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim,qh,kh", [(128, 32, 8), (64, 4, 2), (256, 2, 1), (96, 6, 3)])
-def test_qk_norm_rope(cuda, dtype, head_dim, qh, kh):
+@pytest.mark.parametrize("into_cache", [False, True])
+def test_qk_norm_rope(cuda, dtype, head_dim, qh, kh, into_cache):
     shape = DecoderShape(query_heads=qh, kv_heads=kh, head_dim=head_dim)
     rows = 19
     g = torch.Generator(device=cuda).manual_seed(head_dim + qh)
@@ -57,7 +58,13 @@ def test_qk_norm_rope(cuda, dtype, head_dim, qh, kh):
     qw = (1 + 0.2 * torch.randn(head_dim, generator=g, device=cuda)).to(dtype)
     kw = (1 + 0.2 * torch.randn(head_dim, generator=g, device=cuda)).to(dtype)
     cos, sin = rope_tables(shape, torch.arange(1000, 1000 + rows, device=cuda))
-    q, k = _qk_norm_rope(qkv, qw, kw, cos, sin, shape)
+    if into_cache:  # rows 5..23 of [kv_heads, 40, D] caches, V copied too
+        kc = torch.zeros((kh, 40, head_dim), dtype=dtype, device=cuda)
+        vc = torch.zeros_like(kc)
+        q, k = _qk_norm_rope(qkv, qw, kw, cos, sin, shape, k_out=kc[:, 5:5 + rows],
+                             v_out=vc[:, 5:5 + rows])
+    else:
+        q, k = _qk_norm_rope(qkv, qw, kw, cos, sin, shape)
     torch.cuda.synchronize()
 
     def ref(x, w):  # [rows, H, D]: norm stored in dtype, then rotate-half RoPE
@@ -67,8 +74,16 @@ def test_qk_norm_rope(cuda, dtype, head_dim, qh, kh):
         return (n * cos[:, None] + rot * sin[:, None]).to(dtype)
 
     qd, kd = qh * head_dim, kh * head_dim
-    _close(q, ref(qkv[:, :qd].view(rows, qh, head_dim), qw))
-    _close(k, ref(qkv[:, qd:qd + kd].view(rows, kh, head_dim), kw))
+    assert q.shape == (qh, rows, head_dim) and k.shape == (kh, rows, head_dim)
+    _close(q.transpose(0, 1), ref(qkv[:, :qd].view(rows, qh, head_dim), qw))
+    _close(k.transpose(0, 1), ref(qkv[:, qd:qd + kd].view(rows, kh, head_dim), kw))
+    if into_cache:
+        v = qkv[:, qd + kd:].view(rows, kh, head_dim).transpose(0, 1)
+        assert torch.equal(vc[:, 5:5 + rows], v)
+        assert torch.equal(kc[:, 5:5 + rows], k)
+        # rows outside the written range are untouched
+        assert not kc[:, :5].any() and not kc[:, 5 + rows:].any()
+        assert not vc[:, :5].any() and not vc[:, 5 + rows:].any()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
