@@ -373,7 +373,7 @@ def run_chunked(torch, total: int, chunk: int, alpha: float):
         stock_ms = stock_pass()
     except (RuntimeError, NotImplementedError) as error:  # op missing from this build
         log(f"chunked: stock flash SDPA unavailable: {error}")
-        stock_ms = math.nan
+        stock_ms = None
     del stock
     torch.cuda.empty_cache()
     res = {
@@ -393,10 +393,11 @@ def run_chunked(torch, total: int, chunk: int, alpha: float):
         "density": f_ret / f_dense,
         "retained_tflops_attention": f_ret / (stage["attention"] * 1e-3) / 1e12,
         "stock_sdpa_ms_total": stock_ms,
-        "speedup_vs_stock_sdpa": stock_ms / wall,
+        "speedup_vs_stock_sdpa": None if stock_ms is None else stock_ms / wall,
     }
-    log(f"chunked {total}/{chunk}: stock flash SDPA {stock_ms:.1f} ms "
-        f"({res['speedup_vs_stock_sdpa']:.2f}x slower than FPV2)")
+    if stock_ms is not None:
+        log(f"chunked {total}/{chunk}: stock flash SDPA {stock_ms:.1f} ms "
+            f"({res['speedup_vs_stock_sdpa']:.2f}x slower than FPV2)")
     log(f"chunked {total}/{chunk}: {wall:.1f} ms ({res['tok_per_s']:.0f} tok/s), stages "
         f"{json.dumps({k_: round(v_, 3) for k_, v_ in stage.items()})}; hook-style re-pooling "
         f"{wall_re:.1f} ms, pool {stage_re['pool']:.3f} ms")
