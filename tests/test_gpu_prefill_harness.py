@@ -58,8 +58,9 @@ def _cpu_forward(model: RandomDecoder, tokens: torch.Tensor) -> torch.Tensor:
     return norm(x[-1:], f32(model.final_norm)) @ f32(model.embed).T
 
 
-def test_dense_prefill_matches_float32_cpu(cuda):
-    model = RandomDecoder(SHAPE, device=cuda, seed=3)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dense_prefill_matches_float32_cpu(cuda, dtype):
+    model = RandomDecoder(SHAPE, device=cuda, seed=3, dtype=dtype)
     tokens = torch.randint(0, SHAPE.vocab, (1024,), generator=torch.Generator().manual_seed(4))
     runner = ChunkedPrefillRunner(model, 1024, attention="dense", min_tokens=1)
     got = runner.prefill(tokens.to(cuda), 256).cpu()
@@ -87,10 +88,11 @@ def test_runner_rejects_bad_arguments(cuda):
         runner.prefill(torch.zeros(512, dtype=torch.long, device=cuda), 256)
 
 
-def test_stock_sdpa_prefill_matches_float32_cpu(cuda):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stock_sdpa_prefill_matches_float32_cpu(cuda, dtype):
     """The stock comparison path (torch's flash SDPA op, chunk queries aligned
     to the last keys of the prefix) is exact causal attention too."""
-    model = RandomDecoder(SHAPE, device=cuda, seed=3)
+    model = RandomDecoder(SHAPE, device=cuda, seed=3, dtype=dtype)
     tokens = torch.randint(0, SHAPE.vocab, (1024,), generator=torch.Generator().manual_seed(4))
     runner = ChunkedPrefillRunner(model, 1024, attention="sdpa")
     got = runner.prefill(tokens.to(cuda), 256).cpu()
