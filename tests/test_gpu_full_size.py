@@ -80,3 +80,40 @@ def test_last_tiles_match_oracle_at_full_size(cuda, seq, heavy, planted, n_tiles
         pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
     err = attention_errors(to_np(out[0, :, rows0:rows0 + n_tiles * tq]), ref)
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+def test_maximum_block_count(cuda):
+    """The largest key range the scoring kernel accepts (FPV2_MAX_BLOCKS =
+    8192 blocks, 1 048 576 keys): the last 256 query positions (8 tiles, the
+    last 2 dense) against the whole prefix, high-contrast generator so the
+    correction phase walks thousands of pooled rows per tile."""
+    from fpv2 import _lib
+    seq, lq = _lib.MAX_BLOCKS * 128, 256
+    q, k, v = baseline_qkv(seq, query_heads=8, kv_heads=2, head_dim=128,
+                           planted=3.0 * 128 ** 0.5, heavy_fraction=0.03, seed=1, device=cuda)
+    q = q[:, seq - lq:].contiguous()
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    keep = {}
+    out = _fpv2_sdpa(q[None], k[None], v[None], scale=128 ** -0.5, config=config, keep=keep)
+    torch.cuda.synchronize()
+    cfg = keep["config"]
+    ids, counts, _, _ = keep["lists"]
+    num_blocks = ids.shape[-1]
+    assert num_blocks == _lib.MAX_BLOCKS
+    dev_sel = _device_mask(ids, counts, slice(0, lq // cfg.tile_q), num_blocks)
+
+    ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
+    pooled_k, pooled_v = to_np(keep["pooled_k"]), to_np(keep["pooled_v"])
+    qs = to_np(q)
+    sel, _, ratio = orc.block_scores_and_select(
+        qs, pooled_k, scale=128 ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
+        offset=seq - lq, query_length=lq, return_ratio=True)
+    decided = np.abs(ratio - cfg.alpha) > BAND
+    assert np.array_equal(sel[decided], dev_sel[decided])
+    assert dev_sel[:, :-2].mean() < 0.5  # sparse outside the dense tail
+
+    ref = orc.fpv2_attention_blockwise(
+        qs, to_np(k), to_np(v), scale=128 ** -0.5, selected=dev_sel, pooled_k=pooled_k,
+        pooled_v=pooled_v, config=ocfg, offset=seq - lq, row_block=cfg.tile_q)
+    err = attention_errors(to_np(out[0]), ref)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
