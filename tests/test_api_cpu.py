@@ -315,3 +315,21 @@ def test_decoder_ops_validate_operands_without_a_gpu():
     assert lib.fpv2_add_rms_norm(x, None, 8192, x, _lib.BF16, 1, 8, 8, 0, 8, 1e-6,
                                  None) == _lib.FPV2_ERR_ARGUMENT
     assert b"alias" in lib.fpv2_last_error()
+
+
+def test_score_select_rejects_more_than_the_maximum_block_count():
+    """More than FPV2_MAX_BLOCKS key blocks is refused before any launch."""
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libfpv2_hip.so not built")
+    lib = _lib.load()
+    nb = _lib.MAX_BLOCKS + 1
+    params = _lib.SelectParams(query_heads=8, kv_heads=2, head_dim=128, padded_query_length=32,
+                               query_length=32, num_blocks=nb, key_length=nb * 128,
+                               offset=nb * 128 - 32, block_k=128, tile_q=32, sink_tokens=128,
+                               window_tokens=384, last_n_blocks=2, scale=0.088, alpha=0.1,
+                               q_head_stride=32 * 128, q_row_stride=128,
+                               pooled_head_stride=nb * 128)
+    status = lib.fpv2_score_select(4096, 4096, _lib.BF16, params, None, None, None, None, None,
+                                   None, None)
+    assert status == _lib.FPV2_ERR_UNSUPPORTED
+    assert b"exceeds 8192" in lib.fpv2_last_error()
