@@ -8,13 +8,22 @@ synthetic inputs, already resident in HBM: pool K/V -> score/select/compact
 Primary workload (``value``): BASELINE config 3 at alpha=0.1 — Qwen3-4B
 attention geometry (Hq 32, Hkv 8, D 128), causal prefill of 131072 tokens,
 bf16, block 128, 1 sink block + 384-token window + diagonal, last two query
-tiles dense, correction on.  BASELINE config 2 (32768 tokens) is reported
-beside it under ``at_32k``.  ``value`` is retained TFLOP/s of the whole layer
+tiles dense, correction on.  ``value`` is retained TFLOP/s of the whole layer
 (retained FLOPs / layer time); ``roofline`` is the attention kernel alone,
 timed with HIP events on the stream it runs on.  ``cpu_baseline`` times the
-numpy oracle (selection + attention) on a bounded sample of the same layer.
+numpy oracle's selection and attention on a bounded sample of the same layer.
+
+Reported beside it (each a BASELINE config unless labelled otherwise):
+``at_32k`` (config 2), ``at_32k_no_corr`` (its no-corr ablation),
+``alpha_0.05`` / ``alpha_0.2`` (config 3's sweep), ``contrast_variant`` (the
+sparse regime: planted x 3*sqrt(D), most blocks pruned, correction phase
+active; labelled supplementary), ``chunked_64k`` (config 4), and
+``e2e_qwen3_4b_64k`` (config 5: prefill tok/s and time to first token, FPV2
+vs dense vs stock; ``prefill_tok_per_s`` / ``ttft_s`` at the top level).
 ``stock_sdpa`` (and ``at_32k.stock_sdpa``) times PyTorch-ROCm's fused flash
 attention op on the same inputs, the stock dense path FPV2 replaces.
+``--quick`` skips the secondary configs, ``--profile`` everything but the
+primary layer.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -219,8 +228,20 @@ def _stock_sdpa(torch, data, seq, ms_fpv2, reps=3):
     return res
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (``/proc/cpuinfo``), or "unknown"."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, data, seq, alpha, budget_s: float):
-    """Oracle (numpy) selection + attention on the last tiles of the layer."""
+    """Oracle (numpy) selection and attention on the last tiles of the layer,
+    timed separately; the same tiles' device results are checked against it."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
@@ -247,17 +268,18 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
         for h in range(ids_np.shape[0]):
             for t in range(ids_np.shape[1]):
                 dev_sel[h, t, ids_np[h, t, :counts_np[h, t]]] = True
-        t0 = time.perf_counter()
         with threadpool_limits(limits=cores):
+            t0 = time.perf_counter()
             sel, _, ratio = orc.block_scores_and_select(
                 qs, pooled_k, scale=D ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
                 offset=rows0, query_length=n_tiles * tq, return_ratio=True)
+            t1 = time.perf_counter()
             # attention for the sampled rows on the device's selection (the same
             # work as on the oracle's own), so the output compares like for like
             out = orc.fpv2_attention_blockwise(
                 qs, kn, vn, scale=D ** -0.5, selected=dev_sel, pooled_k=pooled_k,
                 pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
-        dt = time.perf_counter() - t0
+            t2 = time.perf_counter()
         sub = dict(keep, offset=rows0, lists=(ids, counts, pids, pcounts))
         flops, _ = retained_flops(sub, n_tiles * tq, torch)
         decided = np.abs(ratio - cfg.alpha) > 1e-4
@@ -273,21 +295,28 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
         }
         parity["pass"] = (parity["block_mismatches_outside_band"] == 0
                           and parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3)
-        return dt, flops, parity
+        return t1 - t0, t2 - t1, flops, parity
 
-    dt1, f1, _ = sample(1)
-    n = max(1, min(nt, int(budget_s / max(dt1, 1e-3))))
-    log(f"cpu baseline: 1 tile took {dt1:.2f} s; timing the last {n} tiles")
-    dt, flops, parity = sample(n)
+    s1, a1, _, _ = sample(1)
+    n = max(1, min(nt, int(budget_s / max(s1 + a1, 1e-3))))
+    log(f"cpu baseline: 1 tile took {s1 + a1:.2f} s; timing the last {n} tiles")
+    sel_s, attn_s, flops, parity = sample(n)
     log(f"parity of the sampled tiles against the oracle: {json.dumps(parity)}")
     return {
-        "value": flops / dt / 1e12,
+        "value": flops / (sel_s + attn_s) / 1e12,
         "unit": "TFLOP/s",
         "cores": cores,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": (f"numpy oracle (float32, BLAS matmuls on {cores} threads): selection + "
-                   f"attention of the last {n} query tiles ({n * tq} rows x {HQ} heads) of "
-                   f"the seq-{seq} alpha-{alpha} layer; {dt:.1f} s for {flops:.3e} retained FLOP"),
+        "sample": (f"numpy oracle (float64 selection, float32 attention with BLAS matmuls on "
+                   f"{cores} threads) of the last {n} query tiles ({n * tq} rows x {HQ} heads) "
+                   f"of the seq-{seq} alpha-{alpha} layer: selection {sel_s:.2f} s, attention "
+                   f"{attn_s:.2f} s for {flops:.3e} retained FLOP"),
+        "selection_s": sel_s,
+        "attention_s": attn_s,
+        "attention_tflops": flops / attn_s / 1e12,
+        "selection_ms_per_tile": sel_s * 1e3 / n,
+        "attention_ms_per_tile": attn_s * 1e3 / n,
         "parity": parity,
     }
 
@@ -411,26 +440,22 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seq", type=int, default=131072)
     ap.add_argument("--alpha", type=float, default=0.1)
-    ap.add_argument("--secondary-seq", type=int, default=32768,
-                    help="second configuration reported under at_32k (0 skips)")
+    ap.add_argument("--planted", type=float, default=3.0,
+                    help="planted key scale of the primary layer (3.0 is BASELINE's; "
+                         "--planted contrast uses 3*sqrt(D), the sparse contrast variant)",
+                    metavar="X|contrast")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU oracle work for cpu_baseline (0 skips)")
-    ap.add_argument("--extended", action="store_true",
-                    help="also run the 32k no-corr ablation, the 128k alpha sweep and the "
-                         "high-contrast variant")
-    ap.add_argument("--chunked", action="store_true",
-                    help="also run BASELINE config 4 (65536 tokens in 2048-token chunks over a "
-                         "growing KV cache); included in --extended")
-    ap.add_argument("--e2e", action="store_true",
-                    help="also run BASELINE config 5 (random-init Qwen3-4B-architecture "
-                         "prefill of 65536 tokens in 2048-token chunks, FPV2 vs dense); "
-                         "included in --extended")
+    ap.add_argument("--quick", action="store_true",
+                    help="primary layer, 32k layer and CPU baseline only (no alpha sweep, "
+                         "no-corr ablation, contrast variant, chunked or end-to-end runs)")
     ap.add_argument("--profile", action="store_true",
-                    help="primary config only, no CPU baseline (for rocprofv3 runs)")
+                    help="primary layer only, no CPU baseline (for rocprofv3 runs)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES bytes (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters for the traffic figure)")
     args = ap.parse_args(argv)
+    planted = 3.0 * math.sqrt(D) if str(args.planted) == "contrast" else float(args.planted)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -456,31 +481,39 @@ def main(argv=None) -> int:
     from fpv2 import _lib
 
     _lib.load()
-    primary, data = run_config(torch, args.seq, args.alpha, args.steps, args.warmup)
+    primary, data = run_config(torch, args.seq, args.alpha, args.steps, args.warmup,
+                               planted=planted)
     extra = {}
-    if not args.profile and args.secondary_seq:
-        sec, sec_data = run_config(torch, args.secondary_seq, args.alpha, args.steps,
-                                   args.warmup)
-        sec["stock_sdpa"] = stock_sdpa(torch, sec_data, args.secondary_seq, sec["ms_per_layer"])
+    # secondary layers: fewer steps (each is reported, none is `value`)
+    x_steps, x_warm = max(3, min(args.steps, 5)), max(1, min(args.warmup, 2))
+    if not args.profile:
+        sec, sec_data = run_config(torch, 32768, args.alpha, args.steps, args.warmup)
+        sec["stock_sdpa"] = stock_sdpa(torch, sec_data, 32768, sec["ms_per_layer"])
         del sec_data
-        extra["at_32k" if args.secondary_seq == 32768 else f"at_{args.secondary_seq}"] = sec
-    if args.extended and not args.profile:
-        nc, _ = run_config(torch, 32768, args.alpha, args.steps, args.warmup, corr=False)
+        extra["at_32k"] = sec
+    if not args.profile and not args.quick:
+        # BASELINE config 2's ablation, config 3's alpha sweep, and the sparse
+        # regime (contrast variant: planted x 3*sqrt(D), most blocks pruned)
+        nc, _ = run_config(torch, 32768, args.alpha, x_steps, x_warm, corr=False)
         extra["at_32k_no_corr"] = nc
         for a in (0.05, 0.2):
-            r, _ = run_config(torch, args.seq, a, args.steps, args.warmup, heavy=0.03)
+            r, _ = run_config(torch, args.seq, a, x_steps, x_warm, heavy=0.03)
             extra[f"alpha_{a}"] = r
-        c, _ = run_config(torch, args.seq, args.alpha, args.steps, args.warmup,
+        c, _ = run_config(torch, args.seq, args.alpha, x_steps, x_warm,
                           planted=3.0 * math.sqrt(D))
+        c["label"] = ("supplementary contrast variant (not a BASELINE config): planted key "
+                      "direction x 3*sqrt(D) so most blocks are pruned and the correction "
+                      "phase carries the pruned blocks' pooled rows")
         extra["contrast_variant"] = c
-    if (args.extended or args.chunked) and not args.profile:
+        torch.cuda.empty_cache()
         extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
-    if (args.extended or args.e2e) and not args.profile:
+        torch.cuda.empty_cache()
         from fpv2.prefill_harness import QWEN3_4B, measure
         log("e2e: random-init Qwen3-4B-architecture prefill, 65536 tokens, 2048-token chunks")
         e2e = measure(QWEN3_4B, tokens=65536, chunk=2048, alpha=args.alpha, device="cuda:0")
         log(f"e2e: {json.dumps(e2e)}")
         extra["e2e_qwen3_4b_64k"] = e2e
+        torch.cuda.empty_cache()
     if not args.profile:
         extra["stock_sdpa"] = stock_sdpa(torch, data, args.seq, primary["ms_per_layer"])
     cpu = None
@@ -489,6 +522,7 @@ def main(argv=None) -> int:
 
     attn_s = primary["stage_ms"]["attention"] * 1e-3
     traffic, traffic_src = profiled_traffic(args.seq, args.alpha)
+    e2e = extra.get("e2e_qwen3_4b_64k")
     line = {
         "metric": METRIC,
         "value": primary["retained_tflops_layer"],
@@ -501,9 +535,9 @@ def main(argv=None) -> int:
         "scaling": "strong",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: BASELINE generator (N(0,1) Q/K/V, planted unit direction x3.0 on "
-                f"block 0 + {heavy_fraction(args.seq):.0%} of key blocks, 0.5x on queries), "
-                "seed 0, generated on the GPU",
+        "data": f"synthetic: BASELINE generator (N(0,1) Q/K/V, planted unit direction "
+                f"x{planted:.2f} on block 0 + {heavy_fraction(args.seq):.0%} of key blocks, 0.5x "
+                "on queries), seed 0, generated on the GPU",
         "config": {
             "workload": "FPV2 prefill attention layer, Qwen3-4B geometry (Hq 32, Hkv 8, "
                         f"D 128), causal seq {args.seq}, bf16, block 128, alpha {args.alpha}, "
@@ -521,6 +555,9 @@ def main(argv=None) -> int:
         "retained_tflops_attention_kernel": primary["retained_tflops_attention"],
         "mfma_frac_attention_kernel": primary["mfma_frac_attention"],
         "pool_gbs": primary["pool_gbs"],
+        "hbm_frac_pool": primary["hbm_frac_pool"],
+        "prefill_tok_per_s": None if e2e is None else e2e["fpv2"]["prefill_tok_per_s"],
+        "ttft_s": None if e2e is None else e2e["fpv2"]["ttft_s"],
         "roofline": {
             "bound": "mfma",
             "achieved": primary["retained_flops"] / attn_s / 1e12,

@@ -19,9 +19,14 @@ kernels see identical values.
 
 Request rules follow the hook: with ``total_tokens`` known, the dense tail
 applies only once the cache reaches it (``patch.py:55-63``); below
-``min_tokens`` keys the hook hands the call to the original attention, and
-here the same kernels run exact causal attention instead (``alpha = 0`` selects
-every visible block, and with no pruned block the correction is empty).
+``min_tokens`` keys, or with fewer queries than one selection tile, the hook
+hands the call to the original attention (``patch.py:177-205``), and here the
+same kernels run exact causal attention instead (``alpha = 0`` selects every
+visible block, and with no pruned block the correction is empty).
+
+With ``collect_stats`` the layer counts selected and visible blocks as the
+hook's ``block_sparsity`` does (``patch.py:66-88``): selected counts are summed
+on the device, and ``block_sparsity()`` synchronises once to read them.
 """
 
 from __future__ import annotations
@@ -32,8 +37,8 @@ import torch
 
 from fpv2 import _lib
 from fpv2.kernel import SUPPORTED_HEAD_DIMS
-from fpv2.patch import (_effective_config, _geometry, _pool_into, _request_config,
-                        _select_attend)
+from fpv2.patch import (_causal_block_count, _effective_config, _geometry, _pool_into,
+                        _request_config, _select_attend)
 from fpv2.selection import FPV2Config
 
 
@@ -49,7 +54,7 @@ class ChunkedPrefill:
     def __init__(self, query_heads: int, kv_heads: int, head_dim: int, capacity: int, *,
                  dtype: torch.dtype = torch.bfloat16, device: torch.device | str | None = None,
                  config: FPV2Config | None = None, total_tokens: int | None = None,
-                 min_tokens: int = 4_096) -> None:
+                 min_tokens: int = 4_096, collect_stats: bool = False) -> None:
         if kv_heads <= 0 or query_heads <= 0 or query_heads % kv_heads:
             raise ValueError("query heads must be divisible by KV heads")
         if head_dim not in SUPPORTED_HEAD_DIMS:
@@ -90,6 +95,9 @@ class ChunkedPrefill:
         self.length = 0
         self._complete = 0  # leading blocks pooled with all their rows
         self.pooled_rows = 0  # rows read by pooling so far (for accounting)
+        self.collect_stats = collect_stats
+        self._selected = torch.zeros((), dtype=torch.int64, device=device)
+        self._visible = 0
 
     def reset(self) -> None:
         """Empty the caches (a new prompt)."""
@@ -98,6 +106,15 @@ class ChunkedPrefill:
         self.length = 0
         self._complete = 0
         self.pooled_rows = 0
+        self._selected.zero_()
+        self._visible = 0
+
+    def block_sparsity(self) -> float:
+        """Fraction of visible causal blocks skipped by the ``attend`` calls
+        since construction or ``reset`` (0 when nothing was counted)."""
+        if not self._visible:
+            return 0.0
+        return 1.0 - int(self._selected.item()) / self._visible
 
     @staticmethod
     def _three_d(x: torch.Tensor, name: str) -> torch.Tensor:
@@ -150,10 +167,17 @@ class ChunkedPrefill:
                        dtype=dtype, valid_rows=tail, num_blocks=1, block_k=bk, stream=stream)
             self.pooled_rows += tail
 
-    def request_config(self) -> FPV2Config:
-        """The configuration the next ``attend`` uses for the current cache."""
+    def request_config(self, query_length: int | None = None) -> FPV2Config:
+        """The configuration the next ``attend`` uses for the current cache
+        (and, when given, a chunk of ``query_length`` queries).
+
+        The hook sends a call to the original attention when the keys are
+        fewer than ``min_tokens`` or the queries fewer than one tile
+        (``patch.py:177-205``); those calls run exact causal attention here
+        (``alpha = 0``)."""
         config = _request_config(self.config, self.length, self.total_tokens)
-        if self.length < self.min_tokens:
+        if self.length < self.min_tokens or (
+                query_length is not None and query_length < config.tile_q):
             config = replace(config, alpha=0.0)
         return config
 
@@ -174,7 +198,7 @@ class ChunkedPrefill:
         device = _lib.require_device(q3, self.k)
         lib = _lib.load()
         k3, v3 = self.k[:, :self.length], self.v[:, :self.length]
-        geo = _geometry(q3[None], k3[None], v3[None], self.request_config())
+        geo = _geometry(q3[None], k3[None], v3[None], self.request_config(q3.shape[1]))
         with torch.cuda.device(device):
             if marks is not None:
                 marks("pool")
@@ -190,9 +214,15 @@ class ChunkedPrefill:
                              "contiguous last dimension")
         _lib.require_device(out, q3)
         call_scale = self.head_dim ** -0.5 if scale is None else scale
+        if self.collect_stats and keep is None:
+            keep = {}
         _select_attend(q3, k3, v3, self.pooled_k[:, :geo.num_blocks],
                        self.pooled_v[:, :geo.num_blocks], geo, scale=call_scale, out=out,
                        marks=marks, keep=keep)
+        if self.collect_stats:
+            self._selected += keep["lists"][1].sum(dtype=torch.int64)
+            self._visible += _causal_block_count(self.kv_heads, geo.query_length, geo.offset,
+                                                 geo.config)
         return out[None]
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **kwargs) -> torch.Tensor:

@@ -146,10 +146,14 @@ def compact_block_indices(
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """Last dim contiguous, 8-element strides, 16-byte base; else copy."""
+    """Last dim contiguous, 8-element strides, 16-byte base; else copy.
+
+    A view that is contiguous but starts off a 16-byte boundary (a view a
+    few elements into its storage) is cloned: its ``contiguous()`` would
+    return the same misaligned view."""
     if (t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1])
             or t.data_ptr() % 16):
-        t = t.contiguous()
+        t = t.clone(memory_format=torch.contiguous_format)
     return t
 
 
@@ -239,9 +243,11 @@ def _pooled_ready(pooled_k: torch.Tensor, pooled_v: torch.Tensor):
     stride shared by both (a pooled cache with spare capacity is used in
     place)."""
     def ok(p):
-        return p.stride(-1) == 1 and p.stride(-2) == p.shape[-1] and p.stride(0) % 8 == 0
+        return (p.stride(-1) == 1 and p.stride(-2) == p.shape[-1] and p.stride(0) % 8 == 0
+                and p.data_ptr() % 16 == 0)
     if not (ok(pooled_k) and ok(pooled_v) and pooled_k.stride(0) == pooled_v.stride(0)):
-        pooled_k, pooled_v = pooled_k.contiguous(), pooled_v.contiguous()
+        pooled_k = pooled_k.clone(memory_format=torch.contiguous_format)
+        pooled_v = pooled_v.clone(memory_format=torch.contiguous_format)
     return pooled_k, pooled_v
 
 

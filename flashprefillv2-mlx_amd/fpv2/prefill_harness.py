@@ -226,11 +226,16 @@ class ChunkedPrefillRunner:
     ``attention``: ``"fpv2"`` (FPV2 with ``config``), ``"dense"`` (same
     kernels, every visible block) or ``"sdpa"`` (torch's fused flash SDPA
     kernel, the stock dense path).  ``min_tokens`` is the hook's gate: calls
-    with fewer keys attend densely in both modes.
+    with fewer keys attend densely in both modes.  ``collect_stats`` counts
+    selected and visible blocks in every layer (``block_sparsity``).
+    Setting ``capture_layer`` to a layer index keeps that layer's last
+    attention call in ``captured``: its queries, output, cache and block
+    lists (for checking one layer of a full prefill against the oracle).
     """
 
     def __init__(self, model: RandomDecoder, capacity: int, *, attention: str = "fpv2",
-                 config: FPV2Config | None = None, min_tokens: int = 4_096):
+                 config: FPV2Config | None = None, min_tokens: int = 4_096,
+                 collect_stats: bool = False):
         if attention not in ("fpv2", "dense", "sdpa"):
             raise ValueError("attention must be 'fpv2', 'dense' or 'sdpa'")
         s = model.shape
@@ -241,6 +246,8 @@ class ChunkedPrefillRunner:
                               last_n_blocks=base.last_n_blocks,
                               mean_correction=base.mean_correction)
         self.model, self.capacity, self.attention = model, capacity, attention
+        self.capture_layer: int | None = None
+        self.captured: dict | None = None
         if attention == "sdpa":
             self.caches = [_StockAttention(s.query_heads, s.kv_heads, s.head_dim, capacity,
                                            dtype=model.dtype, device=model.device)
@@ -248,12 +255,24 @@ class ChunkedPrefillRunner:
             return
         self.caches = [ChunkedPrefill(s.query_heads, s.kv_heads, s.head_dim, capacity,
                                       dtype=model.dtype, device=model.device, config=base,
-                                      total_tokens=capacity, min_tokens=min_tokens)
+                                      total_tokens=capacity, min_tokens=min_tokens,
+                                      collect_stats=collect_stats)
                        for _ in range(s.layers)]
 
     def reset(self) -> None:
         for cache in self.caches:
             cache.reset()
+
+    def block_sparsity(self) -> float:
+        """Fraction of visible causal blocks skipped over all layers since
+        the last ``reset`` (needs ``collect_stats``; 0 for ``"sdpa"``)."""
+        if self.attention == "sdpa":
+            return 0.0
+        visible = sum(c._visible for c in self.caches)
+        if not visible:
+            return 0.0
+        selected = int(sum(c._selected for c in self.caches).item())
+        return 1.0 - selected / visible
 
     def _layer(self, li: int, x: torch.Tensor, delta: torch.Tensor | None, cos, sin):
         """One decoder layer.  The residual stream is ``x + delta``: the add is
@@ -277,7 +296,10 @@ class ChunkedPrefillRunner:
             k_rows, v_rows = cache.reserve(L)
             q, _ = _qk_norm_rope(qkv, p["q_norm"], p["k_norm"], cos, sin, s,
                                  k_out=k_rows, v_out=v_rows)
-            cache.attend(q, scale=s.head_dim ** -0.5, out=attn_heads)
+            keep = {} if li == self.capture_layer else None
+            cache.attend(q, scale=s.head_dim ** -0.5, out=attn_heads, keep=keep)
+            if keep is not None:
+                self.captured = {"q": q, "out": attn_heads, "cache": cache, "keep": keep}
         h = _add_rms_norm(x, F.linear(attn, p["o"]), p["mlp_norm"], s.rms_eps)
         act = _silu_mul(F.linear(h, p["gate_up"]), s.intermediate)
         return x, F.linear(act, p["down"])
@@ -289,6 +311,12 @@ class ChunkedPrefillRunner:
         n = tokens.numel()
         if n > self.capacity:
             raise ValueError("prompt longer than the KV cache capacity")
+        if self.attention != "sdpa":
+            # the request boundary is this prompt's length, not the cache
+            # capacity (generate.py:101 passes total_tokens=prompt_tokens):
+            # the dense tail applies on the chunk that reaches it
+            for cache in self.caches:
+                cache.total_tokens = n
         x = delta = None
         for start in range(0, n, chunk):
             end = min(start + chunk, n)
@@ -311,7 +339,8 @@ def measure(shape: DecoderShape, *, tokens: int, chunk: int, alpha: float, devic
     logits = {}
     for mode in modes:
         runner = ChunkedPrefillRunner(model, tokens, attention=mode,
-                                      config=FPV2Config(alpha=alpha, sink_tokens=128))
+                                      config=FPV2Config(alpha=alpha, sink_tokens=128),
+                                      collect_stats=mode == "fpv2")
         runner.prefill(prompt[:min(tokens, 2 * chunk)], chunk)  # warm-up
         best = math.inf
         for _ in range(reps):
@@ -323,6 +352,8 @@ def measure(shape: DecoderShape, *, tokens: int, chunk: int, alpha: float, devic
             best = min(best, time.perf_counter() - t0)
         logits[mode] = out
         res[mode] = {"ttft_s": best, "prefill_tok_per_s": tokens / best}
+        if mode == "fpv2":  # over every layer and chunk of the timed prefills
+            res[mode]["block_sparsity"] = runner.block_sparsity()
         del runner
         torch.cuda.empty_cache()
     if "fpv2" in logits and "dense" in logits:

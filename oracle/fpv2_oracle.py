@@ -188,19 +188,33 @@ def block_scores_and_select(q, pooled_k, *, scale: float, config=OracleConfig(),
         tile_ids = np.arange(tile_start, tile_end, dtype=np.int64)
         tile_first = offset + tile_ids * tq
         tile_last = np.minimum(tile_first + tq, offset + valid_length) - 1
-        scores = np.einsum("hgnd,hbd->hgnb", grouped_q[:, :, rows[0]:rows[-1] + 1],
-                           pooled_k) * scale
+        # Blocks starting after the chunk's last valid row are invisible to
+        # every tile of the chunk (not selected, zero energy): only the
+        # leading `nbv` blocks are evaluated (the unchunked call, whose raw
+        # scores are returned, evaluates all of them).
+        nbv = num_blocks
+        if config.score_chunk_tiles is not None:
+            nbv = min(num_blocks, int(tile_last.max()) // config.block_k + 1)
+        # s[h, g, n, b] = q[h, g, n] . k̄[h, b] (selection.py:154-158), as a
+        # batched float64 BLAS product
+        scores = np.matmul(grouped_q[:, :, rows[0]:rows[-1] + 1],
+                           np.swapaxes(pooled_k[:, :nbv], -1, -2)[:, None]) * scale
+        starts, ends = block_starts[:nbv], block_ends[:nbv]
         positions = offset + rows
-        row_visible = (block_starts[None, :] <= positions[:, None]) & (
-            rows[:, None] < valid_length)
+        row_visible = (starts[None, :] <= positions[:, None]) & (rows[:, None] < valid_length)
         tiles = np.where(row_visible[None, None], scores, -np.inf).reshape(
-            kv_heads, group, tile_end - tile_start, tq, num_blocks)
-        fully_visible = block_ends[None, :] <= tile_last[:, None] + 1
+            kv_heads, group, tile_end - tile_start, tq, nbv)
+        fully_visible = ends[None, :] <= tile_last[:, None] + 1
         tiles = np.where(fully_visible[None, None, :, None, :], tiles, -np.inf)
         tile_max = tiles.max(axis=(1, 3, 4), keepdims=True)
+        # exp(s - m) on the visible entries, 0 elsewhere (-inf -> 0)
+        finite = tiles > -np.inf
+        weights = np.zeros(tiles.shape)
         with np.errstate(invalid="ignore"):
-            weights = np.where(tiles > -np.inf, np.exp(tiles - tile_max), 0.0)
-        energies = weights.sum(axis=(1, 3))
+            np.exp(np.subtract(tiles, tile_max, where=finite, out=weights), where=finite,
+                   out=weights)
+        energies = np.zeros((kv_heads, tile_end - tile_start, num_blocks))
+        energies[..., :nbv] = weights.sum(axis=(1, 3))
         max_energy = energies.max(axis=-1, keepdims=True)
         selected = energies >= config.alpha * max_energy
         with np.errstate(invalid="ignore", divide="ignore"):

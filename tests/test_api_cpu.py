@@ -333,3 +333,37 @@ def test_score_select_rejects_more_than_the_maximum_block_count():
                                    None, None)
     assert status == _lib.FPV2_ERR_UNSUPPORTED
     assert b"exceeds 8192" in lib.fpv2_last_error()
+
+
+def test_kernel_ready_realigns_a_contiguous_view_off_a_16_byte_boundary():
+    """A contiguous view whose first element is not 16-byte aligned reaches
+    the C ABI as an aligned copy (``contiguous()`` alone returns the view)."""
+    from fpv2.kernel import _kernel_ready
+    base = torch.arange(2 * 64 * 128 + 8, dtype=torch.bfloat16)
+    view = base[4:4 + 2 * 64 * 128].view(2, 64, 128)  # 8 bytes into the storage
+    assert view.is_contiguous() and view.data_ptr() % 16 == 8
+    ready = _kernel_ready(view)
+    assert ready.data_ptr() % 16 == 0
+    assert ready.stride() == (64 * 128, 128, 1)
+    assert torch.equal(ready, view)
+    aligned = base[8:8 + 2 * 64 * 128].view(2, 64, 128)
+    assert _kernel_ready(aligned).data_ptr() == aligned.data_ptr()  # no copy when aligned
+
+
+def test_chunked_request_config_follows_the_hook_gates():
+    """Below ``min_tokens`` keys or below one tile of queries the hook calls
+    the original attention (``patch.py:177-205``); the chunked layer runs
+    exact attention there (alpha 0), and the dense tail only at
+    ``total_tokens`` (``patch.py:55-63``)."""
+    from fpv2 import ChunkedPrefill
+    cp = ChunkedPrefill.__new__(ChunkedPrefill)  # request rules only: no device state
+    cp.config = FPV2Config(tile_q=32)
+    cp.total_tokens, cp.min_tokens, cp.length = 8192, 4096, 8192
+    assert cp.request_config().alpha == 0.1
+    assert cp.request_config(32).alpha == 0.1
+    assert cp.request_config(31).alpha == 0.0
+    assert cp.request_config(2048).last_n_blocks == 2
+    cp.length = 4095
+    assert cp.request_config(2048).alpha == 0.0
+    cp.length = 6000
+    assert cp.request_config(2048).last_n_blocks == 0

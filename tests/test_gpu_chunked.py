@@ -105,3 +105,81 @@ def test_reserve_then_fill_equals_append(cuda):
         assert torch.equal(x, y)
     with pytest.raises(ValueError, match="capacity"):
         b.reserve(213)
+
+
+def test_chunk_shorter_than_a_tile_is_exact_causal(cuda):
+    """A chunk with fewer queries than one selection tile (here 20 < 32 at
+    G = 4) is sent to the original attention by the hook (``patch.py:177-205``);
+    the chunked layer attends it exactly, also when it is not the last chunk
+    and no ``total_tokens`` is known."""
+    q, k, v = _inputs(cuda, 1320, seed=9)
+    config = FPV2Config(alpha=0.5, sink_tokens=128, window_tokens=128)
+    cp = ChunkedPrefill(8, 2, 128, 1320, config=config, min_tokens=1, device=cuda,
+                        collect_stats=True)
+    cp.step(q[:, :1280], k[:, :1280], v[:, :1280])
+    assert cp.block_sparsity() > 0  # the long chunk prunes
+    short = cp.step(q[:, 1280:1300], k[:, 1280:1300], v[:, 1280:1300])
+    torch.cuda.synchronize()
+    exact = orc.exact_causal_attention(to_np(q[:, 1280:1300]), to_np(k[:, :1300]),
+                                       to_np(v[:, :1300]), 128 ** -0.5, offset=1280)
+    err = attention_errors(to_np(short[0]), exact)
+    assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, err
+
+
+def test_config4_chunked_65536_in_2048_token_chunks(cuda):
+    """one layer, 65536 tokens of the BASELINE generator in
+    2048-token chunks over a growing bf16 KV cache, ``total_tokens`` known.
+    Every chunk equals the hook (``fpv2_sdpa``, which re-pools the whole
+    prefix) bit for bit, the dense tail appears only on the last chunk, and
+    sampled tiles of the last chunk match the oracle on the full prefix:
+    block lists outside the 1e-4 band and rows within 2e-2 / 2e-3."""
+    from fpv2.synthetic import baseline_qkv
+    total, chunk = 65536, 2048
+    q, k, v = baseline_qkv(total, planted=3.0, heavy_fraction=0.06, seed=0, device=cuda)
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    cp = ChunkedPrefill(32, 8, 128, total, config=config, total_tokens=total, min_tokens=2048,
+                        device=cuda)
+    keep = None
+    for s0 in range(0, total, chunk):
+        s1 = s0 + chunk
+        cp.append(k[:, s0:s1], v[:, s0:s1])
+        tail = cp.request_config(chunk).last_n_blocks
+        assert tail == (2 if s1 == total else 0)
+        keep = {}
+        out = cp.attend(q[:, s0:s1], keep=keep)
+        ref = fpv2_sdpa(q[None, :, s0:s1], k[None, :, :s1], v[None, :, :s1], scale=128 ** -0.5,
+                        config=cp.request_config(chunk))
+        assert torch.equal(out, ref), (s0, s1)
+    torch.cuda.synchronize()
+    cfg = keep["config"]
+    tq, off = cfg.tile_q, total - chunk
+    ids, counts, _, _ = keep["lists"]
+    nb = ids.shape[-1]
+    pooled_k = to_np(cp.pooled_k[:, :nb])
+    pooled_v = to_np(cp.pooled_v[:, :nb])
+    kn, vn = to_np(k), to_np(v)
+    assert np.array_equal(pooled_k, orc.pool_blocks(kn, 128, out_dtype="bf16"))
+    assert np.array_equal(pooled_v, orc.pool_blocks(vn, 128, out_dtype="bf16"))
+    ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
+    nt = chunk // tq
+    for t0, n in ((0, 2), (nt // 2, 2), (nt - 3, 3)):  # start, middle, end (dense tail)
+        rows0 = t0 * tq
+        qs = to_np(q[:, off + rows0:off + rows0 + n * tq])
+        # the sampled tiles as their own call at offset off + rows0; the dense
+        # tail counts tiles from the end of the real call
+        sub_cfg = ocfg if t0 + n == nt else orc._replace(ocfg, last_n_blocks=0)
+        sel, _, ratio = orc.block_scores_and_select(
+            qs, pooled_k, scale=128 ** -0.5, config=orc._replace(sub_cfg, score_chunk_tiles=1),
+            offset=off + rows0, query_length=n * tq, return_ratio=True)
+        idn, cn = to_np(ids[:, t0:t0 + n]), to_np(counts[:, t0:t0 + n])
+        dev_sel = np.zeros(idn.shape, dtype=bool)
+        for h in range(idn.shape[0]):
+            for t in range(n):
+                dev_sel[h, t, idn[h, t, :cn[h, t]]] = True
+        decided = np.abs(ratio - cfg.alpha) > 1e-4
+        assert np.array_equal(sel[decided], dev_sel[decided]), t0
+        ref = orc.fpv2_attention_blockwise(
+            qs, kn, vn, scale=128 ** -0.5, selected=dev_sel, pooled_k=pooled_k,
+            pooled_v=pooled_v, config=sub_cfg, offset=off + rows0, row_block=tq)
+        err = attention_errors(to_np(out[0, :, rows0:rows0 + n * tq]), ref)
+        assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (t0, err)
