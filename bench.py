@@ -440,7 +440,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seq", type=int, default=131072)
     ap.add_argument("--alpha", type=float, default=0.1)
-    ap.add_argument("--planted", type=float, default=3.0,
+    ap.add_argument("--planted", default="3.0",
                     help="planted key scale of the primary layer (3.0 is BASELINE's; "
                          "--planted contrast uses 3*sqrt(D), the sparse contrast variant)",
                     metavar="X|contrast")
@@ -455,7 +455,7 @@ def main(argv=None) -> int:
                     help="only run a plain device copy of BYTES bytes (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters for the traffic figure)")
     args = ap.parse_args(argv)
-    planted = 3.0 * math.sqrt(D) if str(args.planted) == "contrast" else float(args.planted)
+    planted = 3.0 * math.sqrt(D) if args.planted == "contrast" else float(args.planted)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -60,6 +60,55 @@ def _cpu_forward(model: RandomDecoder, tokens: torch.Tensor) -> torch.Tensor:
     return norm(x[-1:], f32(model.final_norm)) @ f32(model.embed).T
 
 
+def _float32_forward_gpu(model: RandomDecoder, tokens: torch.Tensor, chunk: int) -> torch.Tensor:
+    """Chunked float32 forward on the GPU with exact causal attention (plain
+    torch float32 matmuls, one KV head at a time), last position's logits."""
+    s, dev = model.shape, model.device
+    L = tokens.numel()
+    g = s.query_heads // s.kv_heads
+    qd, kd, hd = s.query_heads * s.head_dim, s.kv_heads * s.head_dim, s.head_dim
+
+    def norm(x, w):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + s.rms_eps) * w
+
+    embed = model.embed.float()
+    layers = [{k: v.float() for k, v in p.items()} for p in model.layers]
+    kc = [torch.empty((s.kv_heads, L, hd), device=dev) for _ in layers]
+    vc = [torch.empty((s.kv_heads, L, hd), device=dev) for _ in layers]
+    x = None
+    for start in range(0, L, chunk):
+        end = min(start + chunk, L)
+        n = end - start
+        cos, sin = rope_tables(s, torch.arange(start, end, device=dev))
+
+        def rope(t):  # [n, H, D]
+            rot = torch.cat([-t[..., hd // 2:], t[..., :hd // 2]], dim=-1)
+            return t * cos[:, None] + rot * sin[:, None]
+
+        x = embed[tokens[start:end]]
+        causal = torch.arange(end, device=dev)[None, :] > (start + torch.arange(n, device=dev))[:, None]
+        for li, p in enumerate(layers):
+            h = norm(x, p["attn_norm"])
+            qkv = h @ p["qkv"].T
+            q = rope(norm(qkv[:, :qd].view(n, s.query_heads, hd), p["q_norm"]))
+            kc[li][:, start:end] = rope(norm(qkv[:, qd:qd + kd].view(n, s.kv_heads, hd),
+                                             p["k_norm"])).transpose(0, 1)
+            vc[li][:, start:end] = qkv[:, qd + kd:].view(n, s.kv_heads, hd).transpose(0, 1)
+            att = torch.empty((n, s.query_heads, hd), device=dev)
+            for kh in range(s.kv_heads):
+                qh = q[:, kh * g:(kh + 1) * g].transpose(0, 1).reshape(g * n, hd)
+                sc = (qh @ kc[li][kh, :end].T.contiguous()) * hd ** -0.5
+                sc = sc.view(g, n, end).masked_fill_(causal[None], float("-inf"))
+                pr = torch.softmax(sc, dim=-1).view(g * n, end)
+                att[:, kh * g:(kh + 1) * g] = (pr @ vc[li][kh, :end]).view(g, n, hd).transpose(0, 1)
+                del sc, pr
+            x = x + att.reshape(n, qd) @ p["o"].T
+            h = norm(x, p["mlp_norm"])
+            gu = h @ p["gate_up"].T
+            x = x + (torch.nn.functional.silu(gu[:, :s.intermediate]) * gu[:, s.intermediate:]) @ p["down"].T
+    return (norm(x[-1:], model.final_norm.float()) @ embed.T)[0]
+
+
 @pytest.mark.parametrize(("attention", "dtype"), [
     ("dense", torch.bfloat16), ("dense", torch.float16), ("fpv2", torch.bfloat16)])
 def test_prefill_matches_float32_cpu(cuda, attention, dtype):
@@ -174,8 +223,10 @@ def test_config5_full_qwen3_4b_prefill_65536(cuda):
     the stock flash SDPA op.
       * FPV2 logits equal dense bit for bit when every block is selected,
         else within 0.1 of the largest logit;
-      * FPV2 against stock: relative L2 error within 3e-2, max-abs within 0.1
-        of the largest logit, and top-1 agreement up to that bound;
+      * against a float32 forward of the same weights on the GPU, FPV2's
+        relative L2 and max-abs errors are at most 1.25x the stock op's (plus
+        a small margin), and its top-1 is the float32 top-1 up to the stock
+        op's max-abs error;
       * one layer (18) of the last chunk against the oracle on its full
         65536-key prefix: block lists outside the 1e-4 band and sampled
         attention rows within 2e-2 / 2e-3."""
@@ -216,18 +267,20 @@ def test_config5_full_qwen3_4b_prefill_65536(cuda):
         assert torch.equal(lf, ld)
     else:
         assert float((lf - ld).abs().max()) <= 0.1 * float(ld.abs().max())
-    # FPV2 against the stock op: two bf16 implementations of the same forward
-    # whose rounding differences add up over 36 layers and 65536 positions
-    diff = lf - ls
-    stats = {"sparsity": sparsity, "max_abs": float(diff.abs().max()),
-             "max_logit": float(ls.abs().max()),
-             "rel_l2": float(diff.norm() / ls.norm()),
-             "top1_gap": float(ls.max() - ls[int(lf.argmax())])}
-    print(f"config 5 logits: {stats}", flush=True)
-    bound = 0.1 * stats["max_logit"]
-    assert stats["rel_l2"] <= 3e-2, stats
-    assert stats["max_abs"] <= bound, stats
-    assert stats["top1_gap"] <= bound, stats  # top-1 agreement up to the bound
+    # Both bf16 paths against a float32 forward of the same weights: FPV2's
+    # error must not exceed the stock op's by more than a small margin, and
+    # its top-1 must be the float32 top-1 up to the stock path's error.
+    l32 = _float32_forward_gpu(model, prompt, chunk)
+    rel = lambda a: float((a - l32).norm() / l32.norm())  # noqa: E731
+    stats = {"sparsity": sparsity, "rel_l2_fpv2": rel(lf), "rel_l2_stock": rel(ls),
+             "max_abs_fpv2": float((lf - l32).abs().max()),
+             "max_abs_stock": float((ls - l32).abs().max()),
+             "top1_gap_fpv2": float(l32.max() - l32[int(lf.argmax())]),
+             "top1_gap_stock": float(l32.max() - l32[int(ls.argmax())])}
+    print(f"config 5 logits against float32: {stats}", flush=True)
+    assert stats["rel_l2_fpv2"] <= 1.25 * stats["rel_l2_stock"] + 5e-3, stats
+    assert stats["max_abs_fpv2"] <= 1.25 * stats["max_abs_stock"] + 0.05, stats
+    assert stats["top1_gap_fpv2"] <= max(stats["max_abs_stock"], 0.05), stats
 
     ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
     tq, off = cfg.tile_q, tokens - chunk
