@@ -89,6 +89,37 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 
+// O accumulators in AGPRs (the RG = 2 shape): the PV MFMA as inline asm
+// with its C/D operand constrained to AGPRs.  The compiler does not know the
+// asm is an MFMA and inserts no wait states for it, so the code around it
+// supplies them:
+//   * P and V^T operands: the two wait states a VALU write needs before an
+//     MFMA reads the register (the s_nop 1 in front of each MFMA);
+//   * accumulator chains: back-to-back MFMAs on the same C/D registers need
+//     none;
+//   * AGPR reads by VALU (rescale, epilogue) and AGPR writes followed by an
+//     MFMA: agpr_fence(), which names the accumulators as asm operands so no
+//     read or write of them can move across it.
+template <typename T> __device__ __forceinline__ void mfma_agpr(f32x16& acc, u32x4 a, u32x4 b);
+template <> __device__ __forceinline__ void mfma_agpr<bf16_t>(f32x16& acc, u32x4 a, u32x4 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+template <> __device__ __forceinline__ void mfma_agpr<f16_t>(f32x16& acc, u32x4 a, u32x4 b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// 24 wait states: covers the latency of an in-flight 32x32 MFMA before its
+// accumulators are read by VALU, and VALU writes of them before an MFMA.
+template <int DT>
+__device__ __forceinline__ void agpr_fence(f32x16 (&o)[DT]) {
+  static_assert(DT >= 2 && DT <= 4, "2 to 4 accumulator tiles");
+  if constexpr (DT == 2)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]));
+  else if constexpr (DT == 3)
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]));
+  else
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]));
+}
+
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -151,10 +182,14 @@ struct Step {
 // dimension: each multiplies its half of Q and K into a partial S, the two
 // partials are summed through LDS, both compute P, and each accumulates its
 // half of O.  This keeps D = 256 at two waves per SIMD within 256 registers.
-template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
-__global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
+// RG = 2: a wave owns two 32-row groups that share every K/V fragment read
+// from LDS; with the whole 512-entry register file of its SIMD (one wave per
+// SIMD) the two groups' matrix and softmax work interleave within the wave.
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1, int RG = 1>
+__global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ? 2 : 1))) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D>;
   static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0), "D split in halves");
+  static_assert(RG == 1 || (RG == 2 && DS == 1), "two row groups per wave without the D split");
   // asm LDS reads unless a wave's registers do not hold them (D = 256 without
   // the split), where the compiler schedules its LDS reads (see lds_read_b128).
   constexpr bool kAsm = D <= 128 || DS == 2;
@@ -163,7 +198,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = GM::BN;
   constexpr int ROWB = GM::ROWB;
-  constexpr int RW = WAVES / DS * 32;     // packed query rows per workgroup
+  constexpr int RW = WAVES / DS * 32 * RG;  // packed query rows per workgroup
   constexpr int NIK = GM::JT / WAVES;     // fill instructions per wave per sub-tile
   constexpr int NI = 2 * NIK;             // ... per stage (K then V)
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
@@ -189,34 +224,44 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const int last_local = min((t + 1) * a.tq, a.Lq);
   const int abs_last = a.offset + last_local - 1;
 
-  // ---- this lane's query row ----
+  // ---- this lane's query rows (one per row group of the wave) ----
   const int R = a.G * a.tq;
-  const int rwave = wave % (WAVES / DS);  // row group of this wave
+  const int rwave = wave % (WAVES / DS);  // row groups of this wave
   const int dhalf = wave / (WAVES / DS);  // part of the head dimension (DS = 2)
-  const int prow = chunk * RW + rwave * 32 + l32;
-  const bool exists = prow < R;
-  int g = 0, pos = 0;
-  if (exists) {
-    g = prow / a.tq;
-    pos = t * a.tq + (prow - g * a.tq);
+  bool exists[RG], row_valid[RG];
+  int g[RG], pos[RG], qpos_abs[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    const int prow = chunk * RW + (rwave * RG + rg) * 32 + l32;
+    exists[rg] = prow < R;
+    g[rg] = 0;
+    pos[rg] = 0;
+    if (exists[rg]) {
+      g[rg] = prow / a.tq;
+      pos[rg] = t * a.tq + (prow - g[rg] * a.tq);
+    }
+    row_valid[rg] = exists[rg] && pos[rg] < a.Lq;
+    qpos_abs[rg] = a.offset + pos[rg];
   }
-  const bool row_valid = exists && pos < a.Lq;
-  const int qpos_abs = a.offset + pos;
 
-  vec8 qf[KSQ];
+  vec8 qf[RG][KSQ];
   {
     const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
-    const uint32_t qoff =
-        row_valid ? static_cast<uint32_t>((g * a.q_hs + static_cast<int64_t>(pos) * a.q_rs + hf * 8) * 2)
-                  : kOOB;
     // The softmax folds the scale into one FMA per logit and needs a positive
     // factor: for scale < 0 the queries are negated instead (s*c = (-s)*(-c)).
     const uint32_t sign = a.c_scale < 0.f ? 0x80008000u : 0u;
 #pragma unroll
-    for (int k = 0; k < KSQ; ++k) {
-      u32x4 v = buf_load16(qr, qoff + (row_valid ? (dhalf * KSQ + k) * 32 : 0));
-      v ^= sign;
-      qf[k] = as_vec8<T>(v);
+    for (int rg = 0; rg < RG; ++rg) {
+      const uint32_t qoff =
+          row_valid[rg]
+              ? static_cast<uint32_t>((g[rg] * a.q_hs + static_cast<int64_t>(pos[rg]) * a.q_rs + hf * 8) * 2)
+              : kOOB;
+#pragma unroll
+      for (int k = 0; k < KSQ; ++k) {
+        u32x4 v = buf_load16(qr, qoff + (row_valid[rg] ? (dhalf * KSQ + k) * 32 : 0));
+        v ^= sign;
+        qf[rg][k] = as_vec8<T>(v);
+      }
     }
   }
   const float c_pos = fmaxf(fabsf(a.c_scale), 1e-30f);
@@ -430,20 +475,33 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // O / l are rescaled only when some row's max grows past that, so the
   // common case costs no rescale at all.  The result O / l is unchanged.
   constexpr float kRescaleSlack = 8.0f;
-  f32x16 o[DT];
+  f32x16 o[RG][DT];
+  // RG = 2: O lives in AGPRs, accumulated by inline-asm MFMAs (mfma_agpr)
+  constexpr bool kAccA = RG == 2;
 #pragma unroll
-  for (int i = 0; i < DT; ++i) o[i] = f32x16{};
-  float m_ref = neg_inf();
+  for (int rg = 0; rg < RG; ++rg) {
+#pragma unroll
+    for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
+    if constexpr (kAccA) agpr_fence(o[rg]);
+  }
+  float m_ref[RG];
   // Derived from m_ref, updated only when it changes: the exp2 bias
   // (-m_ref, 0 while no key has been seen) and the rescale threshold.  The
   // kernels without correction, and those with D = 256, are at the register
   // limit and recompute them per slice instead of keeping two more live values.
   constexpr bool kKeepRef = CORR && D <= 128;
-  float neg_m = 0.f;
-  float m_thr = neg_inf();
-  auto bias_of_ref = [&]() { return kKeepRef ? neg_m : ((m_ref == neg_inf()) ? 0.f : -m_ref); };
-  auto thr_of_ref = [&]() { return kKeepRef ? m_thr : m_ref + kRescaleSlack; };
-  float l_run = 0.f;
+  float neg_m[RG], m_thr[RG], l_run[RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    m_ref[rg] = neg_inf();
+    neg_m[rg] = 0.f;
+    m_thr[rg] = neg_inf();
+    l_run[rg] = 0.f;
+  }
+  auto bias_of_ref = [&](int rg) {
+    return kKeepRef ? neg_m[rg] : ((m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg]);
+  };
+  auto thr_of_ref = [&](int rg) { return kKeepRef ? m_thr[rg] : m_ref[rg] + kRescaleSlack; };
 
   // LDS read addresses relative to a slice (32 keys of a stage).  K: lane
   // reads row l32, data chunk 2k + hf -> kbase ^ 32k.  V^T: lane j of a
@@ -495,7 +553,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   };
   // S^T of the slice between stages A and B of the pipeline (masked, its max
   // folded into m_ref), in one of two buffers that alternate between slices.
-  f32x16 s_buf[2] = {f32x16{}, f32x16{}};
+  f32x16 s_buf[2][RG];
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) s_buf[0][rg] = s_buf[1][rg] = f32x16{};
   Slice p_pend{0, 0, 0, 0u};
 
   constexpr int PV_OPS = 2 * DT;  // PV MFMAs per slice: (u, dt)
@@ -539,19 +599,25 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   auto needs_mask = [&](const Slice& nw) {
     return nw.nkeys < 32 || (!nw.corr && nw.key0 + 31 > abs_first);
   };
-  auto process_m = [&](auto hn_c, auto hp_c, auto b_c, auto mask_c, const Slice& nw) {
+  // MODE: how the new slice's row max is used (see the walk below)
+  //   0  not computed (the fixed reference of the first pass),
+  //   1  sets the reference (the first slice of the first pass),
+  //   2  online reference with rescale (the exact pass).
+  auto process_m = [&](auto hn_c, auto hp_c, auto b_c, auto mask_c, auto mode_c, const Slice& nw) {
     constexpr bool HN = decltype(hn_c)::value;
     constexpr bool HP = decltype(hp_c)::value;
     constexpr int B = decltype(b_c)::value;
     constexpr bool MASK = decltype(mask_c)::value;
-    f32x16& s_new = s_buf[B];
-    f32x16& s_old = s_buf[1 - B];
+    constexpr int MODE = decltype(mode_c)::value;
+    constexpr bool MAX = HN && MODE != 0;
+    f32x16(&s_new)[RG] = s_buf[B];
+    f32x16(&s_old)[RG] = s_buf[1 - B];
     constexpr int KW = KSQ < 4 ? KSQ : 4;  // K fragment reads in flight
     const uint32_t va = vbase + p_pend.off;
     const uint32_t ka = kbase + nw.off;
     u32x2 vb[2][8];
     u32x4 kf[KSQ];
-    vec8 pb[2];
+    vec8 pb[RG][2];
 
     // ---- stage A ----
     // Wave priority: a wave in the VALU-heavy stage A yields issue to the
@@ -570,31 +636,37 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
         constexpr int i = decltype(ic)::value;
         kf[i] = lds_read_b128<kAsm, 0>(ka ^ (32 * i));
       });
-      s_new = f32x16{};
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) s_new[rg] = f32x16{};
     }
     // V^T batch 0 after the first K window: those K reads do not wait behind it
     if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
     constexpr int NV0 = HP ? 2 * PER_BATCH : 0;  // reads of batch 0
-    float bias = 0.f;
-    if constexpr (HP) {
-      bias = bias_of_ref() + (p_pend.corr ? a.shift : 0.f);
+    float bias[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      bias[rg] = 0.f;
+      if constexpr (HP) bias[rg] = bias_of_ref(rg) + (p_pend.corr ? a.shift : 0.f);
     }
-    u32x4 w[2];
-    // P for the pair of keys (2pi, 2pi+1) of the pending slice
-    auto exp_pair = [&](auto pc) {
-      constexpr int pi = decltype(pc)::value;
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_old[2 * pi], c_pos, bias));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_old[2 * pi + 1], c_pos, bias));
+    u32x4 w[RG][2];
+    // P for the pair of keys (2pi, 2pi+1) of the pending slice in row group
+    // rg, for the pair number f = pi * RG + rg (the row groups alternate)
+    auto exp_pair = [&](auto fc) {
+      constexpr int f = decltype(fc)::value;
+      constexpr int rg = f % RG, pi = f / RG;
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_old[rg][2 * pi], c_pos, bias[rg]));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_old[rg][2 * pi + 1], c_pos, bias[rg]));
       const uint32_t word = pack2<T>(p0, p1);
-      l_run = add_pair<T>(word, l_run);  // row sum of the rounded P used below
-      w[pi / 4][pi % 4] = word;
+      l_run[rg] = add_pair<T>(word, l_run[rg]);  // row sum of the rounded P used below
+      w[rg][pi / 4][pi % 4] = word;
       asm volatile("" ::"v"(word));
     };
+    constexpr int NP = 8 * RG;  // exp pairs per slice
     if constexpr (HN) {
       // kExpLead pairs first, while the first K fragments are in flight,
       // then the rest spread over the QK MFMAs.
-      constexpr int E0 = HP ? kExpLead : 0;
-      constexpr int EA = kExpA;
+      constexpr int E0 = HP ? kExpLead * RG : 0;
+      constexpr int EA = kExpA * RG;
       if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
       StaticFor<0, KSQ>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -605,18 +677,22 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
         constexpr int younger = i < KW ? (Y0 < 15 ? Y0 : 15)
                                        : ((KSQ - 1 - i) < (KW - 1) ? (KSQ - 1 - i) : (KW - 1));
         lgkm_wait<kAsm, younger>(kf[i]);
-        s_new = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[i], s_new);
+#pragma unroll
+        for (int rg = 0; rg < RG; ++rg) s_new[rg] = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[rg][i], s_new[rg]);
         if constexpr (i + KW < KSQ) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
         if constexpr (HP)
           StaticFor<E0 + i * (EA - E0) / KSQ, E0 + (i + 1) * (EA - E0) / KSQ>::run(exp_pair);
       });
     } else if constexpr (HP) {
-      StaticFor<0, 8>::run(exp_pair);
+      StaticFor<0, NP>::run(exp_pair);
     }
-    constexpr int EB = HN ? kExpA : 8;  // pairs done once stage A ends
+    constexpr int EB = HN ? kExpA * RG : NP;  // pairs done once stage A ends
     if constexpr (HP) {
-      pb[0] = as_vec8<T>(w[0]);
-      if constexpr (EB == 8) pb[1] = as_vec8<T>(w[1]);
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        pb[rg][0] = as_vec8<T>(w[rg][0]);
+        if constexpr (EB == NP) pb[rg][1] = as_vec8<T>(w[rg][1]);
+      }
     }
 
     // DS = 2: add the partner's partial S (every wave of the workgroup takes
@@ -627,13 +703,13 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       const f32x4* theirs = reinterpret_cast<const f32x4*>(xbuf + (wave ^ (WAVES / 2)) * 4096) + lane;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        mine[j * 64] = f32x4{s_new[4 * j], s_new[4 * j + 1], s_new[4 * j + 2], s_new[4 * j + 3]};
+        mine[j * 64] = f32x4{s_new[0][4 * j], s_new[0][4 * j + 1], s_new[0][4 * j + 2], s_new[0][4 * j + 3]};
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 v = theirs[j * 64];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s_new[4 * j + e] += v[e];
+        for (int e = 0; e < 4; ++e) s_new[0][4 * j + e] += v[e];
       }
     }
 
@@ -643,12 +719,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       // it is kept iff e < nkeys and (correction, or e <= qpos - key0), i.e.
       // iff c_j <= lim with one per-lane limit, so the 16 tests compare
       // against immediates.
-      int lim = nw.nkeys - 1 - hf * 4;
-      if (!nw.corr) lim = min(lim, qpos_abs - nw.key0 - hf * 4);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int cj = (j >> 2) * 8 + (j & 3);
-        s_new[j] = cj <= lim ? s_new[j] : neg_inf();
+      for (int rg = 0; rg < RG; ++rg) {
+        int lim = nw.nkeys - 1 - hf * 4;
+        if (!nw.corr) lim = min(lim, qpos_abs[rg] - nw.key0 - hf * 4);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int cj = (j >> 2) * 8 + (j & 3);
+          s_new[rg][j] = cj <= lim ? s_new[rg][j] : neg_inf();
+        }
       }
     }
 
@@ -656,11 +735,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     __builtin_amdgcn_s_setprio(1);
     // PV MFMAs of the pending slice with the row max of the new one spread
     // over them.
-    float mx = neg_inf();
-    auto max_step = [&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      mx = fmaxf(fmaxf(mx, s_new[2 * j]), s_new[2 * j + 1]);
-      asm volatile("" : "+v"(mx));
+    float mx[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) mx[rg] = neg_inf();
+    // max of the key pair (2j, 2j+1) of row group rg, step f = j * RG + rg
+    auto max_step = [&](auto fc) {
+      constexpr int f = decltype(fc)::value;
+      constexpr int rg = f % RG, j = f / RG;
+      mx[rg] = fmaxf(fmaxf(mx[rg], s_new[rg][2 * j]), s_new[rg][2 * j + 1]);
+      asm volatile("" : "+v"(mx[rg]));
     };
     if constexpr (HP) {
       lgkm_wait<kAsm, 0>(vb[0]);
@@ -674,53 +757,70 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
             constexpr int u = op / DT, dt = op % DT;
             const u32x2(&r)[8] = vb[b & 1];
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
-            o[dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[u], o[dt]);
-            if constexpr (EB < 8 && op < DT) {
-              StaticFor<EB + op * (8 - EB) / DT, EB + (op + 1) * (8 - EB) / DT>::run(exp_pair);
-              if constexpr (op + 1 == DT) pb[1] = as_vec8<T>(w[1]);
+#pragma unroll
+            for (int rg = 0; rg < RG; ++rg) {
+              if constexpr (kAccA) mfma_agpr<T>(o[rg][dt], av, __builtin_bit_cast(u32x4, pb[rg][u]));
+              else o[rg][dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[rg][u], o[rg][dt]);
+            }
+            if constexpr (EB < NP && op < DT) {
+              StaticFor<EB + op * (NP - EB) / DT, EB + (op + 1) * (NP - EB) / DT>::run(exp_pair);
+              if constexpr (op + 1 == DT) {
+#pragma unroll
+                for (int rg = 0; rg < RG; ++rg) pb[rg][1] = as_vec8<T>(w[rg][1]);
+              }
             }
             // the row max starts kMaxDelay MFMAs in, when S^T has landed
             constexpr int DM = kMaxDelay < PV_OPS ? kMaxDelay : PV_OPS - 1;
-            if constexpr (HN && op >= DM)
-              StaticFor<(op - DM) * 8 / (PV_OPS - DM), (op - DM + 1) * 8 / (PV_OPS - DM)>::run(max_step);
+            if constexpr (MAX && op >= DM)
+              StaticFor<(op - DM) * NP / (PV_OPS - DM), (op - DM + 1) * NP / (PV_OPS - DM)>::run(max_step);
           }
         });
         if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
       });
-    } else if constexpr (HN) {
-      StaticFor<0, 8>::run(max_step);
-    }
-    float m_cand = neg_inf();
-    if constexpr (HN) {
-      mx = pair_max(mx);
-      m_cand = fmaf(mx, c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
+    } else if constexpr (MAX) {
+      StaticFor<0, NP>::run(max_step);
     }
 
     // ---- stage C: reference max of the new slice ----
-    if constexpr (HN) {
-      if (__ballot(m_cand > thr_of_ref()) != 0ull) {
-        const float m_new = fmaxf(m_ref, m_cand);
-        const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-        m_ref = m_new;
-        if constexpr (kKeepRef) {
-          neg_m = (m_ref == neg_inf()) ? 0.f : -m_ref;
-          m_thr = m_ref + kRescaleSlack;
-        }
-        l_run *= alpha;
+    if constexpr (MAX && MODE == 1) {
+      // the first slice: O and l are still zero, no rescale
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) scale_in_place(o[dt], alpha);
+      for (int rg = 0; rg < RG; ++rg) {
+        m_ref[rg] = fmaf(pair_max(mx[rg]), c_pos, nw.corr ? a.shift : 0.f);
+        neg_m[rg] = (m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg];
+        m_thr[rg] = m_ref[rg] + kRescaleSlack;
       }
-      p_pend = nw;
     }
+    if constexpr (MAX && MODE == 2) {
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        const float m_cand = fmaf(pair_max(mx[rg]), c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
+        if (__ballot(m_cand > thr_of_ref(rg)) != 0ull) {
+          const float m_new = fmaxf(m_ref[rg], m_cand);
+          const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
+          m_ref[rg] = m_new;
+          if constexpr (kKeepRef) {
+            neg_m[rg] = (m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg];
+            m_thr[rg] = m_ref[rg] + kRescaleSlack;
+          }
+          l_run[rg] *= alpha;
+          if constexpr (kAccA) agpr_fence(o[rg]);
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) scale_in_place(o[rg][dt], alpha);
+          if constexpr (kAccA) agpr_fence(o[rg]);
+        }
+      }
+    }
+    if constexpr (HN) p_pend = nw;
   };
   // The mask decision is taken before the call so that stages A and B stay
   // free of branches.
-  auto process = [&](auto hn_c, auto hp_c, auto b_c, const Slice& nw) {
+  auto process = [&](auto hn_c, auto hp_c, auto b_c, auto mode_c, const Slice& nw) {
     if constexpr (decltype(hn_c)::value) {
-      if (needs_mask(nw)) process_m(hn_c, hp_c, b_c, std::true_type{}, nw);
-      else process_m(hn_c, hp_c, b_c, std::false_type{}, nw);
+      if (needs_mask(nw)) process_m(hn_c, hp_c, b_c, std::true_type{}, mode_c, nw);
+      else process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, nw);
     } else {
-      process_m(hn_c, hp_c, b_c, std::false_type{}, nw);
+      process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, nw);
     }
   };
 
@@ -728,76 +828,127 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // while the fills of the next LA sub-tiles are in flight.  Fills past the
   // end load an empty sub-tile so every iteration issues the same number of
   // fills. ----
-  Step pend[LA];
-#pragma unroll
-  for (int p = 0; p < LA; ++p) {
-    pend[p] = next_step();
-    fill_step(pend[p], p);
-  }
   using True = std::integral_constant<bool, true>;
   using False = std::integral_constant<bool, false>;
-  int cstage = 0;
-  // One sub-tile (one slice).  The pending slice enters in s_buf[P] and
-  // leaves in s_buf[1-P].
-  auto do_step = [&](auto first_c, auto p_c) {
-    constexpr bool FIRST = decltype(first_c)::value;
-    constexpr int P = decltype(p_c)::value;
-    using NewB = std::integral_constant<int, 1 - P>;
-    using PendB = std::integral_constant<int, P>;
-    fills_done();  // sub-tile it is in LDS; sub-tile it-2's stage is free
-    const Step cur = pend[0];
-#pragma unroll
-    for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
-    pend[LA - 1] = next_step();
-    const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
-    fill_step(pend[LA - 1], fstage);
-    const Slice s0 = make_slice(cur, cstage, 0);
-    if constexpr (FIRST) process(True{}, False{}, NewB{}, s0);
-    else process(True{}, True{}, NewB{}, s0);
-    cstage = cstage == NST - 1 ? 0 : cstage + 1;
-  };
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  if (n_steps > 0) {
-    do_step(True{}, P0{});  // the first sub-tile has no pending slice
-    // the pending buffer alternates, so two sub-tiles per iteration
-    int it = 1;
-    for (; it + 1 < n_steps; it += 2) {
-      do_step(False{}, P1{});
-      do_step(False{}, P0{});
+  auto run_walk = [&](auto online_c) {
+    constexpr bool ONLINE = decltype(online_c)::value;
+    using MFirst = std::integral_constant<int, ONLINE ? 2 : 1>;
+    using MRest = std::integral_constant<int, ONLINE ? 2 : 0>;
+    Step pend[LA];
+#pragma unroll
+    for (int p = 0; p < LA; ++p) {
+      pend[p] = next_step();
+      fill_step(pend[p], p);
     }
-    if (it < n_steps) {
-      do_step(False{}, P1{});
-      process(False{}, True{}, P1{}, p_pend);  // pending in s_buf[0]
-    } else {
-      process(False{}, True{}, P0{}, p_pend);  // pending in s_buf[1]
+    int cstage = 0;
+    // One sub-tile (one slice).  The pending slice enters in s_buf[P] and
+    // leaves in s_buf[1-P].
+    auto do_step = [&](auto first_c, auto p_c) {
+      constexpr bool FIRST = decltype(first_c)::value;
+      constexpr int P = decltype(p_c)::value;
+      using NewB = std::integral_constant<int, 1 - P>;
+      fills_done();  // sub-tile it is in LDS; sub-tile it-2's stage is free
+      const Step cur = pend[0];
+#pragma unroll
+      for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
+      pend[LA - 1] = next_step();
+      const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
+      fill_step(pend[LA - 1], fstage);
+      const Slice s0 = make_slice(cur, cstage, 0);
+      if constexpr (FIRST) process(True{}, False{}, NewB{}, MFirst{}, s0);
+      else process(True{}, True{}, NewB{}, MRest{}, s0);
+      cstage = cstage == NST - 1 ? 0 : cstage + 1;
+    };
+    if (n_steps > 0) {
+      do_step(True{}, P0{});  // the first sub-tile has no pending slice
+      // the pending buffer alternates, so two sub-tiles per iteration
+      int it = 1;
+      for (; it + 1 < n_steps; it += 2) {
+        do_step(False{}, P1{});
+        do_step(False{}, P0{});
+      }
+      if (it < n_steps) {
+        do_step(False{}, P1{});
+        process(False{}, True{}, P1{}, MRest{}, p_pend);  // pending in s_buf[0]
+      } else {
+        process(False{}, True{}, P0{}, MRest{}, p_pend);  // pending in s_buf[1]
+      }
     }
+    // No fill may land in LDS after the walk ends.
+    vm_wait<0>();
+  };
+
+  // First pass: each row's reference is the max of its first slice and is
+  // never updated, so the walk computes no row max and never rescales O.
+  // P = exp2(s*c - m_ref) may then exceed 1 by any factor: float32 sums and
+  // bfloat16 P hold it unless the range is exceeded.  A valid row whose sum
+  // leaves [2^-60, 2^100] (or is NaN) sends the workgroup through the walk
+  // again with the online reference and rescale (kernel.py:287-310).
+  run_walk(False{});
+  bool bad = false;
+#pragma unroll
+  for (int rg = 0; rg < RG; ++rg) {
+    const float l = pair_sum(l_run[rg]);
+    bad = bad || (row_valid[rg] && !(l >= 0x1p-60f && l <= 0x1p100f));
   }
-  // No fill may land in LDS after the workgroup ends.
-  vm_wait<0>();
+  // Workgroup-wide decision through the last ring stage, which the second
+  // walk refills only after its first barrier (the flags are read by then).
+  int* const flags = reinterpret_cast<int*>(smem + (NST - 1) * GM::STAGE);
+  __syncthreads();  // every wave is done with the ring
+  const int wave_bad = __ballot(bad) != 0ull;  // every lane votes, then lane 0 stores
+  if (lane == 0) flags[wave] = wave_bad;
+  __syncthreads();
+  int redo = 0;
+#pragma unroll
+  for (int w = 0; w < WAVES; ++w) redo |= flags[w];
+  if (redo) {
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) {
+      if constexpr (kAccA) agpr_fence(o[rg]);
+#pragma unroll
+      for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
+      if constexpr (kAccA) agpr_fence(o[rg]);
+      m_ref[rg] = neg_inf();
+      neg_m[rg] = 0.f;
+      m_thr[rg] = neg_inf();
+      l_run[rg] = 0.f;
+    }
+    p_pend = Slice{0, 0, 0, 0u};
+    walk_it = 0;
+    win_base = 0;
+    window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
+    if constexpr (CORR) pids_lanes = lane < pr_count ? pid_lane : 0;
+    run_walk(True{});
+  }
 
   // ---- normalise and store ----
-  const float l_tot = pair_sum(l_run);
-  if (!exists || pos >= a.out_rows) return;
-  const float inv = (row_valid && l_tot > 0.f) ? 1.f / l_tot : 0.f;
-  uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g) * a.o_hs + pos * a.o_rs;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
+  for (int rg = 0; rg < RG; ++rg) {
+    if constexpr (kAccA) agpr_fence(o[rg]);
+    const float l_tot = pair_sum(l_run[rg]);
+    if (!exists[rg] || pos[rg] >= a.out_rows) continue;
+    const float inv = (row_valid[rg] && l_tot > 0.f) ? 1.f / l_tot : 0.f;
+    uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g[rg]) * a.o_hs + pos[rg] * a.o_rs;
 #pragma unroll
-    for (int jg = 0; jg < 4; ++jg) {
-      const int d0 = (dhalf * DT + dt) * 32 + jg * 8 + hf * 4;
-      u32x2 w;
-      w[0] = pack2<T>(o[dt][jg * 4 + 0] * inv, o[dt][jg * 4 + 1] * inv);
-      w[1] = pack2<T>(o[dt][jg * 4 + 2] * inv, o[dt][jg * 4 + 3] * inv);
-      *reinterpret_cast<u32x2*>(orow + d0) = w;
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg) {
+        const int d0 = (dhalf * DT + dt) * 32 + jg * 8 + hf * 4;
+        u32x2 wv;
+        wv[0] = pack2<T>(o[rg][dt][jg * 4 + 0] * inv, o[rg][dt][jg * 4 + 1] * inv);
+        wv[1] = pack2<T>(o[rg][dt][jg * 4 + 2] * inv, o[rg][dt][jg * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d0) = wv;
+      }
     }
   }
 }
 
-template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1, int RG = 1>
 int launch_attn(AttnArgs a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS>;
-  constexpr int RW = WAVES / DS * 32;
+  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS, RG>;
+  constexpr int RW = WAVES / DS * 32 * RG;
   a.nchunk = (a.G * a.tq + RW - 1) / RW;
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
   if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
@@ -811,9 +962,14 @@ int launch_attn(AttnArgs a, hipStream_t stream) {
 // between 256 rows, was measured no faster at 512-row tiles and up to 17 %
 // slower at 256-row tiles.)  D = 256: 8 waves for 128 rows, two per 32-row
 // group each owning half of D (DS = 2), 160 KiB.
+#ifndef FPV2_ROW_GROUPS
+#define FPV2_ROW_GROUPS 1
+#endif
 template <typename T, int D, bool CORR>
 int launch_shape(const AttnArgs& a, hipStream_t s) {
-  if constexpr (D <= 128) {
+  if constexpr (D <= 128 && FPV2_ROW_GROUPS == 2) {
+    return launch_attn<T, D, CORR, 2, 4, 1, 2>(a, s);
+  } else if constexpr (D <= 128) {
     return launch_attn<T, D, CORR, 4, 4>(a, s);
   } else {
     return launch_attn<T, D, CORR, 8, 4, 2>(a, s);

@@ -186,3 +186,51 @@ def test_out_of_range_lists_are_clipped(cuda):
     out = sparse_attention(q, k, v, pk, pv, ids, cnt, pids, pcnt, scale=0.125, config=config)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
+
+
+def _planted_outlier(length, *, strength, seed, hq=8, hkv=2, d=128):
+    """N(0,1) Q/K/V plus one key (position length * 5 // 8 of each KV head)
+    aligned with every later query: its logit exceeds the rest of the row by
+    about strength**2 / sqrt(d) nats."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((hq, length, d), generator=g)
+    k = torch.randn((hkv, length, d), generator=g)
+    v = torch.randn((hkv, length, d), generator=g)
+    u = torch.randn((hkv, d), generator=g)
+    u = u / u.norm(dim=-1, keepdim=True)
+    j = length * 5 // 8
+    k[:, j] = strength * u
+    q[:, j:] += strength * u.repeat_interleave(hq // hkv, dim=0)[:, None, :]
+    return q, k, v
+
+
+@pytest.mark.parametrize(("strength", "what"), [
+    # logit gap ~140 nats (~200 in log2): float32 exp2 overflows against the
+    # first slice's reference, so the workgroup takes the online-rescale walk
+    (40.0, "overflow"),
+    # gap ~50 nats (~70 in log2): P far above 1, within float32 / bf16 range,
+    # no second walk
+    (24.0, "large"),
+])
+def test_logits_far_above_the_first_slice(cuda, strength, what):
+    """Rows whose largest logit comes late in the walk and far above every
+    key of the first slice: attention still matches the oracle.  The fixed
+    first-slice reference either holds the range or sends the workgroup
+    through the online-reference walk (kernel.py:287-310 rescales per key
+    block instead)."""
+    q, k, v = _planted_outlier(1024, strength=strength, seed=21)
+    config = FPV2Config(alpha=0.0, sink_tokens=0, window_tokens=0, last_n_blocks=0,
+                        mean_correction=False, tile_q=32)
+    got, _ = _run_and_check(cuda, q, k, v, config)
+    exact = orc.exact_causal_attention(to_np(q.bfloat16()), to_np(k.bfloat16()),
+                                       to_np(v.bfloat16()), 128 ** -0.5)
+    err = attention_errors(got, exact)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+def test_outlier_with_correction_phase(cuda):
+    """The same late outlier with pruning and mean correction on (alpha 0.5):
+    the second walk repeats the exact and the correction phases."""
+    q, k, v = _planted_outlier(2048, strength=40.0, seed=22)
+    config = FPV2Config(alpha=0.5, sink_tokens=128, window_tokens=128, tile_q=32)
+    _run_and_check(cuda, q, k, v, config)
