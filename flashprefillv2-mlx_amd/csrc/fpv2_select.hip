@@ -419,13 +419,16 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_mfma_kern
 // buffer_load_dwordx4 ... lds kAhead chunks ahead, so the workgroup reads each
 // chunk from L2 once and no wave waits on a global load in the loop.  Every
 // wave multiplies every chunk (S = Q . Kbar^T, a lane holds 16 rows of one
-// block) and reduces its rows to per-block (max, sum) partials; the four
-// waves' partials of a chunk are merged into (c_b, e_b) one chunk later by
-// one wave, through a double-buffered LDS slot.
+// block) and sums its rows' 2^(x - m_w) per block against a lazily updated
+// wave reference m_w (x = s*log2(e)); one wave adds the four waves' partials
+// into the block energies E_b one chunk later, each partial scaled by
+// 2^(m_w - G) for the workgroup reference G.  Energies are only compared
+// with each other (E_b >= alpha * max E), so any common reference gives the
+// same selection as exp(s - max) (selection.py:178-185).
 // LDS (dynamic only, so that the ring starts at LDS address 0 and its rows
-// are aligned for the XOR-swizzled reads): ring [kRing][32][ROWB] (reused
-// for the flag arrays), c_b[Nb], e_b[Nb], partials [2][4][32] x (c, e),
-// row positions [128], reduction scratch.
+// are aligned for the XOR-swizzled reads): ring [kRing][32][ROWB], E_b[Nb],
+// partials [2 slots][4 waves][32 blocks], their references [2][4], G, row
+// positions [128], reduction scratch.
 // ---------------------------------------------------------------------------
 template <int D>
 struct RingGeom {
@@ -443,13 +446,109 @@ struct RingGeom {
 };
 constexpr int kAhead = 2;           // chunks filled ahead of the multiply
 constexpr int kRing = kAhead + 1;   // ring stages
+// A wave's reference m_w is raised only when a chunk's logit exceeds it by
+// more than kWaveSlack (log2 units), and G only when some m_w exceeds it by
+// more than kGroupSlack: a partial is at most 32 * 2^kWaveSlack and its
+// merge factor at most 2^kGroupSlack, far inside float32.
+constexpr float kWaveSlack = 16.f;
+constexpr float kGroupSlack = 30.f;
 
 template <int D>
 constexpr size_t ring_lds_bytes(int64_t Nb) {
-  return (static_cast<size_t>(kRing) * RingGeom<D>::TILE > static_cast<size_t>(Nb) * 2
-              ? static_cast<size_t>(kRing) * RingGeom<D>::TILE
-              : static_cast<size_t>(Nb) * 2) +
-         static_cast<size_t>(Nb) * 8 + 2 * 4 * 32 * 8 + kRowsPerPass * 4 + 16 + 32;
+  return static_cast<size_t>(kRing) * RingGeom<D>::TILE + static_cast<size_t>(Nb) * 4 +
+         (2 * 4 * 32 + 2 * 4 + 4) * 4 + kRowsPerPass * 4 + 16 * 4;
+}
+
+__device__ __forceinline__ float wave_max_any(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+// Mask and lists from the block energies (selection.py:183-195 and
+// kernel.py:141-184) in 32-bit arithmetic (the host routes geometries whose
+// key positions need more bits elsewhere).  Wave w compacts the blocks
+// [w * span, (w + 1) * span) 64 at a time with ballots: one pass counts, the
+// waves' counts are exchanged through LDS, a second pass writes each block's
+// positions (selected ascending, then the rest ascending; likewise pruned).
+__device__ void finish_ring(const SelectArgs& a, int h, int t, int tile_first, int tile_last,
+                            int nfv, const float* eb, float* fred, int* ired) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int Nb = static_cast<int>(a.Nb);
+  float emax = 0.f;
+  for (int b = tid; b < nfv; b += kThreads) emax = fmaxf(emax, eb[b]);
+  emax = block_max(emax, fred);
+  const float thr = a.alpha * emax;
+  const int bk = static_cast<int>(a.bk);
+  const int sink = static_cast<int>(a.sink);
+  const int first_minus_window = tile_first - static_cast<int>(a.window);
+  const int lk = static_cast<int>(a.Lk);
+  const bool tail = t >= a.Nt - a.last_n;
+  // branch-free: every lane reads an E_b (clamped index; entries past nfv
+  // are discarded), so no LDS read is left pending in a divergent branch
+  auto flags = [&](int b, bool& sel, bool& pru) {
+    const float e_raw = eb[min(b, Nb - 1)];
+    const float E = b < nfv ? e_raw : 0.f;
+    const int bs = b * bk;
+    const int be = bs + bk;
+    const bool forced = bs < sink || be > first_minus_window || tail;
+    sel = (E >= thr || forced) && bs <= tile_last;
+    pru = !sel && min(be, lk) <= tile_first;
+  };
+  const int span = ((Nb + 4 * 64 - 1) / (4 * 64)) * 64;
+  const int w0 = min(Nb, wave * span), w1 = min(Nb, w0 + span);
+  int ns = 0, np = 0;
+  for (int base = w0; base < w1; base += 64) {
+    const int b = base + lane;
+    bool sel, pru;
+    flags(b, sel, pru);
+    sel = sel && b < w1;
+    pru = pru && b < w1;
+    ns += __popcll(__ballot(sel));
+    np += __popcll(__ballot(pru));
+  }
+  if (lane == 0) {
+    ired[wave] = ns;
+    ired[4 + wave] = np;
+  }
+  __syncthreads();
+  int run_s = 0, run_p = 0, tot_s = 0, tot_p = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int cs = ired[w], cp = ired[4 + w];
+    run_s += w < wave ? cs : 0;
+    run_p += w < wave ? cp : 0;
+    tot_s += cs;
+    tot_p += cp;
+  }
+  const int64_t row = static_cast<int64_t>(h) * a.Nt + t;
+  int32_t* ids = a.ids + row * a.Nb;
+  int32_t* pids = a.pids + row * a.Nb;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = w0; base < w1; base += 64) {
+    const int b = base + lane;
+    bool sel, pru;
+    flags(b, sel, pru);
+    sel = sel && b < w1;
+    pru = pru && b < w1;
+    const uint64_t ms = __ballot(sel);
+    const uint64_t mp = __ballot(pru);
+    if (b < w1) {
+      const int ps = run_s + __popcll(ms & below);  // selected before b
+      const int pp = run_p + __popcll(mp & below);
+      ids[sel ? ps : tot_s + (b - ps)] = b;
+      pids[pru ? pp : tot_p + (b - pp)] = b;
+      if (a.sel_out) a.sel_out[row * a.Nb + b] = sel;
+    }
+    run_s += __popcll(ms);
+    run_p += __popcll(mp);
+  }
+  if (tid == 0) {
+    a.counts[row] = tot_s;
+    a.pcounts[row] = tot_p;
+  }
 }
 
 template <typename T, int D>
@@ -459,11 +558,11 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
   extern __shared__ __align__(1024) unsigned char smem[];
   constexpr size_t kRingBytes = static_cast<size_t>(kRing) * GM::TILE;
-  const size_t flag_bytes = static_cast<size_t>(a.Nb) * 2;
-  float* cb = reinterpret_cast<float*>(smem + (kRingBytes > flag_bytes ? kRingBytes : flag_bytes));
-  float* eb = cb + a.Nb;
-  float* xpart = eb + a.Nb;  // [2 slots][4 waves][32 blocks] c, then the same for e
-  int* rpos = reinterpret_cast<int*>(xpart + 512);  // local query position, -1: no such row
+  float* eb = reinterpret_cast<float*>(smem + kRingBytes);  // block energies, reference G
+  float* xe = eb + a.Nb;     // [2 slots][4 waves][32 blocks] chunk partials
+  float* xm = xe + 256;      // [2 slots][4 waves] their wave references
+  float* gref = xm + 8;      // G
+  int* rpos = reinterpret_cast<int*>(gref + 4);  // local query position, -1: no such row
   float* fred = reinterpret_cast<float*>(rpos + kRowsPerPass);
   int* ired = reinterpret_cast<int*>(fred + 4);
 
@@ -478,11 +577,11 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
   const int nchunks = (nfv + 31) / 32;
   const float sc2 = a.scale * kLog2e;  // > 0 on this path
   const int lq = static_cast<int>(a.Lq);
+  const int offset = static_cast<int>(a.offset);
+  const int bk = static_cast<int>(a.bk);
 
-  for (int b = tid; b < nfv; b += kThreads) {
-    cb[b] = neg_inf();
-    eb[b] = 0.f;
-  }
+  for (int b = tid; b < nfv; b += kThreads) eb[b] = 0.f;
+  if (tid == 0) *gref = neg_inf();
 
   // ---- fills: chunk c of the pooled keys into ring stage c % kRing ----
   // Fill instruction i of this wave covers LDS bytes [1024 j, 1024 (j + 1))
@@ -501,7 +600,6 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
     fill_row[i] = row;
     fill_off[i] = c < GM::DG ? (row * D + c * 8) * 2 : -1;
   }
-  const uint32_t ring_lds = lds_addr(smem);
   auto fill_chunk = [&](int c) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     uint8_t* const sp = smem + (c % kRing) * GM::TILE;
@@ -513,32 +611,38 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
     }
   };
   // K fragment k of the lane's block row l32 (data chunk 2k + hf)
-  const uint32_t kread = (ring_lds + l32 * GM::ROWB + ((16 * hf) ^ (16 * GM::kmask(l32))));
+  const uint32_t kread = (lds_addr(smem) + l32 * GM::ROWB + ((16 * hf) ^ (16 * GM::kmask(l32))));
 
-  // merge the four waves' partials of chunk c (slot c & 1) into c_b / e_b
-  // (one common max, then five independent terms)
+  // add the four waves' partials of chunk c (slot c & 1) to E_b (lanes 0-31
+  // of wave c & 3); G follows the largest wave reference with a slack, and
+  // the energies merged so far are rescaled when it moves (rare)
   auto merge_chunk = [&](int c) {
     if (lane < 32 && wave == (c & 3)) {
+      const float* xms = xm + (c & 1) * 4;
+      const float m0 = xms[0], m1 = xms[1], m2 = xms[2], m3 = xms[3];
+      const float mc = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
+      float g = *gref;
+      if (mc > g + kGroupSlack) {  // uniform over the merging lanes
+        const float f = (g == neg_inf()) ? 0.f : exp2_fast(g - mc);
+        for (int b = lane; b < nfv; b += 32) eb[b] *= f;
+        g = mc;
+        if (lane == 0) *gref = g;
+      }
       const int b = c * 32 + lane;
       if (b < nfv) {
-        const float* xc = xpart + (c & 1) * 128 + lane;
-        const float* xe = xpart + 256 + (c & 1) * 128 + lane;
-        float cv[5] = {cb[b], xc[0], xc[32], xc[64], xc[96]};
-        float ev[5] = {eb[b], xe[0], xe[32], xe[64], xe[96]};
-        float m = cv[0];
-#pragma unroll
-        for (int i = 1; i < 5; ++i) m = fmaxf(m, cv[i]);
-        if (m != neg_inf()) {
-          float e = 0.f;
-#pragma unroll
-          for (int i = 0; i < 5; ++i) e += (cv[i] == neg_inf()) ? 0.f : ev[i] * exp2_fast(cv[i] - m);
-          cb[b] = m;
-          eb[b] = e;
-        }
+        const float* xc = xe + (c & 1) * 128 + lane;
+        float e = eb[b];
+        if (m0 != neg_inf()) e = fmaf(xc[0], exp2_fast(m0 - g), e);
+        if (m1 != neg_inf()) e = fmaf(xc[32], exp2_fast(m1 - g), e);
+        if (m2 != neg_inf()) e = fmaf(xc[64], exp2_fast(m2 - g), e);
+        if (m3 != neg_inf()) e = fmaf(xc[96], exp2_fast(m3 - g), e);
+        eb[b] = e;
       }
     }
   };
 
+  float mref = neg_inf();    // wave reference m_w (log2 units, wave-uniform)
+  float thr_raw = neg_inf(); // raw score above which m_w must move: (m_w + slack) / sc2
   for (int64_t rc = 0; rc < R; rc += kRowsPerPass) {
     __syncthreads();  // the previous pass is done with the ring and rpos
     if (tid < kRowsPerPass) {
@@ -599,60 +703,59 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
       // Lane holds rows (j/4)*8 + hf*4 + j%4 of the wave's 32 rows, block b.
       const int b = c * 32 + l32;
       const bool b_scored = b < nfv;
-      const int lo = static_cast<int>(max<int64_t>(0, static_cast<int64_t>(b) * a.bk - a.offset));
-      float cmax = neg_inf(), esum = 0.f;
+      const int lo = max(0, b * bk - offset);
+      float e = 0.f;
       if (__ballot(!(b_scored && g_lo >= lo && g_hi < lq)) == 0ull) {
         // every row sees the block: no per-row tests
-        float mx = acc[0];
+        float lm = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
 #pragma unroll
-        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, acc[j]);
-        cmax = mx * sc2;
+        for (int j = 3; j < 15; j += 2) lm = fmaxf(fmaxf(lm, acc[j]), acc[j + 1]);
+        lm = fmaxf(lm, acc[15]);
+        if (__ballot(lm > thr_raw) != 0ull) {  // rare: raise the wave reference
+          mref = wave_max_any(lm) * sc2;
+          thr_raw = (mref + kWaveSlack) / sc2;
+        }
+        const float bias = -mref;
         float e0 = 0.f, e1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 16; j += 2) {
-          e0 += exp2_fast(fmaf(acc[j], sc2, -cmax));
-          e1 += exp2_fast(fmaf(acc[j + 1], sc2, -cmax));
+          e0 += exp2_fast(fmaf(acc[j], sc2, bias));
+          e1 += exp2_fast(fmaf(acc[j + 1], sc2, bias));
         }
-        esum = e0 + e1;
+        e = e0 + e1;
       } else {
-        float sv[16];
         bool ok[16];
+        float lm = neg_inf();
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int pos = rpos[wave * 32 + (j >> 2) * 8 + hf * 4 + (j & 3)];
-          sv[j] = acc[j] * sc2;
           ok[j] = b_scored && pos >= lo && pos < lq;
-          if (ok[j]) cmax = fmaxf(cmax, sv[j]);
+          if (ok[j]) lm = fmaxf(lm, acc[j]);
         }
-        if (cmax != neg_inf()) {
+        if (__ballot(lm > thr_raw) != 0ull) {
+          mref = wave_max_any(lm) * sc2;
+          thr_raw = (mref + kWaveSlack) / sc2;
+        }
+        const float bias = -mref;
 #pragma unroll
-          for (int j = 0; j < 16; ++j)
-            if (ok[j]) esum += exp2_fast(sv[j] - cmax);
-        }
+        for (int j = 0; j < 16; ++j)
+          if (ok[j]) e += exp2_fast(fmaf(acc[j], sc2, bias));
       }
-      // partner lane (hf ^ 1) holds the other 16 rows: one v_permlane32_swap
-      // per value hands each lane both halves
+      // partner lane (hf ^ 1) holds the other 16 rows of the block
       {
-        const auto cs = __builtin_amdgcn_permlane32_swap(__float_as_uint(cmax), __float_as_uint(cmax), false, false);
-        const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(esum), __float_as_uint(esum), false, false);
-        cmax = __uint_as_float(cs[0]);
-        esum = __uint_as_float(es[0]);
-        merge_ce(cmax, esum, __uint_as_float(cs[1]), __uint_as_float(es[1]));
+        const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(e), __float_as_uint(e), false, false);
+        e = __uint_as_float(es[0]) + __uint_as_float(es[1]);
       }
-      if (hf == 0) {
-        xpart[(c & 1) * 128 + wave * 32 + l32] = cmax;
-        xpart[256 + (c & 1) * 128 + wave * 32 + l32] = esum;
-      }
+      if (hf == 0) xe[(c & 1) * 128 + wave * 32 + l32] = e;
+      if (lane == 0) xm[(c & 1) * 4 + wave] = mref;
     }
     vm_wait<0>();  // the fills past the last chunk
     __syncthreads();
     if (nchunks > 0) merge_chunk(nchunks - 1);
   }
   __syncthreads();
-  // The ring is free now: reuse it for the flag arrays.
-  uint8_t* fsel = smem;
-  uint8_t* fpr = fsel + a.Nb;
-  finish_tile(a, ti, cb, eb, fsel, fpr, fred, ired);
+  finish_ring(a, static_cast<int>(ti.h), static_cast<int>(ti.t), static_cast<int>(ti.tile_first),
+              static_cast<int>(ti.tile_last), nfv, eb, fred, ired);
 }
 
 // ---------------------------------------------------------------------------
@@ -789,7 +892,10 @@ int launch_generic(K kernel, dim3 grid, size_t lds, hipStream_t stream, const Se
 template <typename T>
 int dispatch_mfma(int64_t D, dim3 grid, hipStream_t stream, const SelectArgs& a, bool* done) {
   *done = true;
-  if (a.scores == nullptr && a.scale > 0.f) {
+  // the ring kernel keeps key positions and list entries in 32 bits
+  const bool small = a.Nb * a.bk <= (1LL << 30) && a.offset + a.Lq_pad <= (1LL << 30) &&
+                     a.sink <= (1LL << 30) && a.window <= (1LL << 30) && a.Nt <= (1LL << 30);
+  if (a.scores == nullptr && a.scale > 0.f && a.ids != nullptr && small) {
     switch (D) {
       case 64: return launch_with_lds(select_ring_kernel<T, 64>, grid, ring_lds_bytes<64>(a.Nb), stream, a);
       case 96: return launch_with_lds(select_ring_kernel<T, 96>, grid, ring_lds_bytes<96>(a.Nb), stream, a);
