@@ -278,7 +278,6 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   const int cnt_raw = a.counts[list_row];
   const int pcnt_raw = CORR ? a.pcounts[list_row] : 0;
   const int id_lane = clampi(ids[min(lane, Nb - 1)], 0, Nb - 1);  // entry `lane`
-  const int pid_lane = CORR ? clampi(pids[min(lane, Nb - 1)], 0, Nb - 1) : 0;
   const int sel_count = clampi(cnt_raw, 0, Nb);
   const int pr_count = CORR ? clampi(pcnt_raw, 0, Nb) : 0;
   const int subs = (a.bk + BN - 1) / BN;
@@ -328,9 +327,8 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // Exact steps are described 64 at a time: lane j of a window holds the
   // first key and valid-row count of step win_base + j, computed in one
   // vector pass from the selected list, and a step reads its pair with two
-  // readlanes.  Correction steps follow from the step index; the pruned list
-  // is read 64 entries per VGPR and handed to the fill lanes with
-  // ds_bpermute.
+  // readlanes.  Correction steps follow from the step index; each lane loads
+  // the pruned-list entries of its own fill rows one step ahead.
   int win_base = 0, win_key0 = 0, win_nk = 0;
   auto window_entry = [&](int it, int blk) {
     const int li = it / subs;
@@ -348,8 +346,6 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // the first window's entries come from id_lane (its steps cover at most
   // the first 64 entries)
   window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
-  int pids_lanes = 0;
-  if constexpr (CORR) pids_lanes = lane < pr_count ? pid_lane : 0;
   int walk_it = 0;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
@@ -400,6 +396,19 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     pre[i] = c < GM::DG ? (row * rs + c * 8) * 2 : -1;
   }
   const uint32_t smem_lds = lds_addr(smem);
+  // Correction fills take their pooled rows' block ids from cid: the pruned
+  // list entries li + fill_row(j, lane) of the next correction step (li),
+  // loaded one step ahead (the first step's here), so that no fill address
+  // waits on a load or a lane exchange.
+  int cid[NIK];
+  auto load_cids = [&](int li) {
+#pragma unroll
+    for (int j = 0; j < NIK; ++j) {
+      const int e = li + fill_row(j, lane);
+      cid[j] = (CORR && e < pr_count) ? clampi(pids[e], 0, Nb - 1) : 0;
+    }
+  };
+  load_cids(0);
   auto fill_step = [&](const Step& s, int stage) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     // (a lambda returning an LDS pointer would drop the kernel from the host
@@ -431,29 +440,19 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
         }
       }
     } else {  // correction: pooled rows of the pruned blocks
-      const int w0 = s.li & 63;  // first entry within pids_lanes
-      // When this step uses up the window, the next 64 entries are fetched
-      // before this step's fills are issued: the wait for them, right after
-      // the load, then covers only the older fills (issued a step earlier),
-      // not the ones below.
-      int next_lanes = pids_lanes;
-      if (((s.li + BN) & 63) == 0) {
-        const int li = s.li + BN + lane;
-        next_lanes = li < pr_count ? clampi(pids[li], 0, Nb - 1) : 0;
-      }
       const int ln = opaque_lane();
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int row = fill_row(i, ln);
         const int c = fill_chunk(i, row, ln);
-        const int blk = __builtin_amdgcn_ds_bpermute((w0 + row) * 4, pids_lanes);
+        const int blk = cid[i % NIK];  // entry s.li + row, loaded a step earlier
         const bool ok = row < s.nkeys && c < GM::DG;
         const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             i < NIK ? pkr : pvr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
             16, off, 0, 0, 0);
       }
-      pids_lanes = next_lanes;
+      load_cids(s.li + BN);  // the next correction step's entries
     }
   };
   // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
@@ -919,7 +918,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     walk_it = 0;
     win_base = 0;
     window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
-    if constexpr (CORR) pids_lanes = lane < pr_count ? pid_lane : 0;
+    load_cids(0);
     run_walk(True{});
   }
 

@@ -444,7 +444,10 @@ struct RingGeom {
     return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
   }
 };
-constexpr int kAhead = 2;           // chunks filled ahead of the multiply
+#ifndef FPV2_SEL_AHEAD
+#define FPV2_SEL_AHEAD 2
+#endif
+constexpr int kAhead = FPV2_SEL_AHEAD;  // chunks filled ahead of the multiply
 constexpr int kRing = kAhead + 1;   // ring stages
 // A wave's reference m_w is raised only when a chunk's logit exceeds it by
 // more than kWaveSlack (log2 units), and G only when some m_w exceeds it by
