@@ -1,8 +1,8 @@
 """Static check of the kernels' asynchronous LDS reads.
 
-The sparse-attention kernel and the ring path of the selection kernel issue
-their LDS reads as inline asm (the compiler would otherwise serialise them
-behind the asynchronous global->LDS fills) and
+The sparse-attention kernel and the owner path (head_dim 256) of the
+selection kernel issue their LDS reads as inline asm (the compiler would
+otherwise serialise them behind the asynchronous global->LDS fills) and
 waits for them with ``s_waitcnt lgkmcnt(N)``.  The compiler treats the result
 register of such a read as written when the asm statement ends, so nothing
 stops it from copying or spilling that register before the data has arrived.

@@ -33,6 +33,7 @@ struct SelectArgs {
   int32_t* counts;
   int32_t* pids;
   int32_t* pcounts;
+  uint32_t tq_magic;  // ceil(2^32 / tq), streaming path
 };
 
 struct TileInfo {
@@ -205,7 +206,7 @@ __device__ void finish_tile(const SelectArgs& a, const TileInfo& ti, float* cb, 
 // ---------------------------------------------------------------------------
 // Score-output path: bf16 / f16 queries and pooled keys, head_dim D (multiple
 // of 16), taken when the caller asks for the scores or the scale is not
-// positive (the ring path below serves the rest).  Each wave owns 32-block
+// positive (the streaming and owner paths below serve the rest).  Each wave owns 32-block
 // chunks of pooled keys in VGPRs and loops over the pass's row groups.
 // LDS: Q pass [128][D+8] (reused for the flag arrays), c_b[Nb], e_b[Nb].
 // ---------------------------------------------------------------------------
@@ -412,60 +413,43 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_mfma_kern
 }
 
 // ---------------------------------------------------------------------------
-// Ring path: bf16 / f16, head_dim D (multiple of 16), positive scale, no
-// score output -- the hook's path.  Wave w owns the 32 packed rows
-// [32w, 32w + 32) of each 128-row pass, its Q fragments in VGPRs.  The pooled
-// keys stream through an LDS ring of 32-block chunks filled by
-// buffer_load_dwordx4 ... lds kAhead chunks ahead, so the workgroup reads each
-// chunk from L2 once and no wave waits on a global load in the loop.  Every
-// wave multiplies every chunk (S = Q . Kbar^T, a lane holds 16 rows of one
-// block) and sums its rows' 2^(x - m_w) per block against a lazily updated
-// wave reference m_w (x = s*log2(e)); one wave adds the four waves' partials
-// into the block energies E_b one chunk later, each partial scaled by
-// 2^(m_w - G) for the workgroup reference G.  Energies are only compared
-// with each other (E_b >= alpha * max E), so any common reference gives the
-// same selection as exp(s - max) (selection.py:178-185).
-// LDS (dynamic only, so that the ring starts at LDS address 0 and its rows
-// are aligned for the XOR-swizzled reads): ring [kRing][32][ROWB], E_b[Nb],
-// partials [2 slots][4 waves][32 blocks], their references [2][4], G, row
-// positions [128], reduction scratch.
+// Shared by the hook's paths (bf16 / f16, head_dim a multiple of 16, positive
+// scale, no score output).  Block energies are sums of 2^(x - m_w), x =
+// s * log2(e), against a lazily raised per-wave reference m_w, rescaled to a
+// common reference before the selection.  Energies are only compared with
+// each other (E_b >= alpha * max E), so any common reference gives the same
+// selection as exp(s - max) (selection.py:178-185).
 // ---------------------------------------------------------------------------
-template <int D>
-struct RingGeom {
-  static constexpr int ROWB = D <= 64 ? 128 : (D <= 128 ? 256 : 512);  // LDS row (power of two)
-  static constexpr int RC = ROWB / 16;      // 16-byte chunks per LDS row
-  static constexpr int DG = D / 8;          // chunks holding data
-  static constexpr int TILE = 32 * ROWB;    // one 32-block chunk
-  static constexpr int NF = TILE / 1024 / (kThreads / 64);  // fill instructions per wave per chunk
-  static_assert(TILE % (1024 * (kThreads / 64)) == 0, "fills split evenly over the waves");
-  // 16-byte chunk c of row r is stored at chunk c ^ kmask(r): the 16 rows of
-  // a ds_read_b128 quarter-wave then hit 16 different 16-byte bank groups
-  static __device__ __forceinline__ int kmask(int row) {
-    return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
-  }
-};
-#ifndef FPV2_SEL_AHEAD
-#define FPV2_SEL_AHEAD 2
-#endif
-constexpr int kAhead = FPV2_SEL_AHEAD;  // chunks filled ahead of the multiply
-constexpr int kRing = kAhead + 1;   // ring stages
-// A wave's reference m_w is raised only when a chunk's logit exceeds it by
-// more than kWaveSlack (log2 units), and G only when some m_w exceeds it by
-// more than kGroupSlack: a partial is at most 32 * 2^kWaveSlack and its
-// merge factor at most 2^kGroupSlack, far inside float32.
+// A wave's reference m_w is raised only when a logit exceeds it by more than
+// kWaveSlack (log2 units): a row group's sum is at most 16 * 2^kWaveSlack
+// per lane, far inside float32.
 constexpr float kWaveSlack = 16.f;
-constexpr float kGroupSlack = 30.f;
-
-template <int D>
-constexpr size_t ring_lds_bytes(int64_t Nb) {
-  return static_cast<size_t>(kRing) * RingGeom<D>::TILE + static_cast<size_t>(Nb) * 4 +
-         (2 * 4 * 32 + 2 * 4 + 4) * 4 + kRowsPerPass * 4 + 16 * 4;
-}
 
 __device__ __forceinline__ float wave_max_any(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
   return v;
+}
+
+// The same without LDS traffic: DPP within 16-lane rows (quad permutes,
+// then half-row and row mirrors), permlane swaps across rows and halves.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {
+      case 0xB1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
+      case 0x4E: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xF, 0xF, false));
+      case 0x141: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xF, 0xF, false));
+      default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xF, 0xF, false));
+    }
+  };
+  v = fmaxf(v, dpp(v, 0xB1));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp(v, 0x4E));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp(v, 0x141));  // row_half_mirror: the other quad of the half-row
+  v = fmaxf(v, dpp(v, 0x140));  // row_mirror: the other half of the row
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));  // rows 0+1, 2+3
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));  // both halves
 }
 
 // Mask and lists from the block energies (selection.py:183-195 and
@@ -474,7 +458,7 @@ __device__ __forceinline__ float wave_max_any(float v) {
 // [w * span, (w + 1) * span) 64 at a time with ballots: one pass counts, the
 // waves' counts are exchanged through LDS, a second pass writes each block's
 // positions (selected ascending, then the rest ascending; likewise pruned).
-__device__ void finish_ring(const SelectArgs& a, int h, int t, int tile_first, int tile_last,
+__device__ __forceinline__ void finish_lists(const SelectArgs& a, int h, int t, int tile_first, int tile_last,
                             int nfv, const float* eb, float* fred, int* ired) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -554,18 +538,42 @@ __device__ void finish_ring(const SelectArgs& a, int h, int t, int tile_first, i
   }
 }
 
+// ---------------------------------------------------------------------------
+// Owner path: the hook's path for D = 256 (the streaming path below keeps a
+// unit's Q in registers, which D = 256 leaves no room for).  The tile's packed rows are staged in LDS once
+// per 128-row pass; wave w owns the 32-block chunks c = w, w + 4, ... and, for
+// each, multiplies all row groups of the pass with the chunk's pooled keys,
+// which it loads straight from L2 into registers one of its chunks ahead.  A
+// block's energy is summed entirely by its owner wave against the wave's lazy
+// reference m_w, so no partials are merged across waves; before the
+// selection every wave rescales its blocks by 2^(m_w - G), G = max m_w.
+// LDS: Q pass [128][D + 8] (padded rows: conflict-free 16-byte column
+// reads), E_b[Nb], wave references [4], row positions [128], scratch.
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr size_t own_lds_bytes(int64_t Nb) {
+  return static_cast<size_t>(kRowsPerPass) * (D + 8) * 2 + kRowsPerPass * 8 + static_cast<size_t>(Nb) * 4 +
+         4 * 4 + kRowsPerPass * 4 + 16 * 4;
+}
+
+// A row group's 16 scores per lane sum to at most 16 * 2^kWaveSlack while no
+// score exceeds the wave reference by more than kWaveSlack; a sum above
+// kRaiseSum therefore means some score exceeds it by more than kWaveSlack - 4,
+// and the reference is raised to the wave's largest score before the sum is
+// taken again.
+constexpr float kRaiseSum = 65536.f;  // 2^kWaveSlack
+static_assert(kWaveSlack == 16.f, "kRaiseSum is 2^kWaveSlack");
+
 template <typename T, int D>
-__global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kernel(SelectArgs a) {
-  using GM = RingGeom<D>;
-  using vec8 = typename Elem<T>::vec8;
+__global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(1, 2))) void select_own_kernel(SelectArgs a) {
   constexpr int KS = D / 16;  // MFMA k-steps over the head dimension
-  extern __shared__ __align__(1024) unsigned char smem[];
-  constexpr size_t kRingBytes = static_cast<size_t>(kRing) * GM::TILE;
-  float* eb = reinterpret_cast<float*>(smem + kRingBytes);  // block energies, reference G
-  float* xe = eb + a.Nb;     // [2 slots][4 waves][32 blocks] chunk partials
-  float* xm = xe + 256;      // [2 slots][4 waves] their wave references
-  float* gref = xm + 8;      // G
-  int* rpos = reinterpret_cast<int*>(gref + 4);  // local query position, -1: no such row
+  constexpr int LDQ = D + 8;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* qs = reinterpret_cast<uint16_t*>(smem);
+  int64_t* qoff = reinterpret_cast<int64_t*>(smem + static_cast<size_t>(kRowsPerPass) * LDQ * 2);  // row -> q element, -1: zeros
+  float* eb = reinterpret_cast<float*>(qoff + kRowsPerPass);
+  float* xm = eb + a.Nb;  // [4] wave references
+  int* rpos = reinterpret_cast<int*>(xm + 4);  // local query position, -1: no such row
   float* fred = reinterpret_cast<float*>(rpos + kRowsPerPass);
   int* ired = reinterpret_cast<int*>(fred + 4);
 
@@ -584,181 +592,754 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 3 : 2)) void select_ring_kern
   const int bk = static_cast<int>(a.bk);
 
   for (int b = tid; b < nfv; b += kThreads) eb[b] = 0.f;
-  if (tid == 0) *gref = neg_inf();
 
-  // ---- fills: chunk c of the pooled keys into ring stage c % kRing ----
-  // Fill instruction i of this wave covers LDS bytes [1024 j, 1024 (j + 1))
-  // of the stage, j = wave + 4 i: lane -> row (64 j + lane) / RC, stored
-  // chunk p = (64 j + lane) % RC, holding data chunk p ^ kmask(row).  Blocks
-  // past nfv and pad chunks past D load zeros.
+  // K-bar fragment k of a chunk: the lane's block row c*32 + l32, data chunk
+  // 2k + hf (16 bytes, immediate offset 32 k); blocks past nfv read zeros
   const rsrc_t pkr = make_rsrc(static_cast<const uint16_t*>(a.pk) + ti.h * a.pk_hs,
                                static_cast<uint32_t>(a.Nb * D * 2));
-  int fill_off[GM::NF];  // byte offset within the chunk's 32 rows (-1: pad)
-  int fill_row[GM::NF];
+  auto load_kbar = [&](int c, u32x4 (&kf)[KS]) {
+    const int b = c * 32 + l32;
+    const uint32_t base = (c < nchunks && b < nfv) ? static_cast<uint32_t>((b * D + hf * 8) * 2) : kOOB;
 #pragma unroll
-  for (int i = 0; i < GM::NF; ++i) {
-    const int e = 64 * (wave + 4 * i) + lane;
-    const int row = e / GM::RC;
-    const int c = (e % GM::RC) ^ GM::kmask(row);
-    fill_row[i] = row;
-    fill_off[i] = c < GM::DG ? (row * D + c * 8) * 2 : -1;
-  }
-  auto fill_chunk = [&](int c) {
-    typedef __attribute__((address_space(3))) void* lds_ptr;
-    uint8_t* const sp = smem + (c % kRing) * GM::TILE;
+    for (int k = 0; k < KS; ++k) kf[k] = buf_load16(pkr, base + k * 32);
+  };
+  // S = Q . Kbar^T for row group rg of the pass: a lane holds rows
+  // (j/4)*8 + hf*4 + j%4 of the group, block c*32 + l32
+  const uint16_t* qrow = qs + l32 * LDQ + hf * 8;
+  auto load_q = [&](int rg, u32x4 (&qf)[KS]) {
 #pragma unroll
-    for (int i = 0; i < GM::NF; ++i) {
-      const bool ok = c < nchunks && c * 32 + fill_row[i] < nfv && fill_off[i] >= 0;
-      const uint32_t off = ok ? static_cast<uint32_t>(c * 32 * D * 2 + fill_off[i]) : kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(sp + (wave + 4 * i) * 1024), 16, off, 0, 0, 0);
-    }
+    for (int k = 0; k < KS; ++k) qf[k] = load16(qrow + rg * 32 * LDQ + k * 16);
   };
-  // K fragment k of the lane's block row l32 (data chunk 2k + hf)
-  const uint32_t kread = (lds_addr(smem) + l32 * GM::ROWB + ((16 * hf) ^ (16 * GM::kmask(l32))));
-
-  // add the four waves' partials of chunk c (slot c & 1) to E_b (lanes 0-31
-  // of wave c & 3); G follows the largest wave reference with a slack, and
-  // the energies merged so far are rescaled when it moves (rare)
-  auto merge_chunk = [&](int c) {
-    if (lane < 32 && wave == (c & 3)) {
-      const float* xms = xm + (c & 1) * 4;
-      const float m0 = xms[0], m1 = xms[1], m2 = xms[2], m3 = xms[3];
-      const float mc = fmaxf(fmaxf(m0, m1), fmaxf(m2, m3));
-      float g = *gref;
-      if (mc > g + kGroupSlack) {  // uniform over the merging lanes
-        const float f = (g == neg_inf()) ? 0.f : exp2_fast(g - mc);
-        for (int b = lane; b < nfv; b += 32) eb[b] *= f;
-        g = mc;
-        if (lane == 0) *gref = g;
-      }
-      const int b = c * 32 + lane;
-      if (b < nfv) {
-        const float* xc = xe + (c & 1) * 128 + lane;
-        float e = eb[b];
-        if (m0 != neg_inf()) e = fmaf(xc[0], exp2_fast(m0 - g), e);
-        if (m1 != neg_inf()) e = fmaf(xc[32], exp2_fast(m1 - g), e);
-        if (m2 != neg_inf()) e = fmaf(xc[64], exp2_fast(m2 - g), e);
-        if (m3 != neg_inf()) e = fmaf(xc[96], exp2_fast(m3 - g), e);
-        eb[b] = e;
-      }
-    }
+  auto mma = [&](const u32x4 (&qf)[KS], const u32x4 (&kf)[KS]) {
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < KS; ++k) acc = Elem<T>::mfma32(as_vec8<T>(qf[k]), as_vec8<T>(kf[k]), acc);
+    return acc;
+  };
+  auto qk = [&](int rg, const u32x4 (&kf)[KS]) {
+    u32x4 qf[KS];
+    load_q(rg, qf);
+    return mma(qf, kf);
+  };
+  // the same by inline-asm reads: fragment k of group RG at a fixed offset
+  // from the lane's row of group 0
+#ifndef FPV2_SEL_KPRE
+#define FPV2_SEL_KPRE 0
+#endif
+  constexpr bool kResident = D <= 128;  // Q of the pass held in registers
+  constexpr bool kPrefetch = FPV2_SEL_KPRE != 0 && D <= 128;
+  const uint32_t qaddr = lds_addr(qrow);
+  auto read_q = [&](auto rgc, u32x4 (&qf)[KS]) {
+    constexpr int rg = decltype(rgc)::value;
+    StaticFor<0, KS>::run([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      qf[k] = lds_read_b128<true, (rg * 32 * LDQ + k * 16) * 2>(qaddr);
+    });
+  };
+  auto mma_wait = [&](u32x4 (&qf)[KS], const u32x4 (&kf)[KS]) {
+    f32x16 acc = {};
+    StaticFor<0, KS>::run([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      constexpr int younger = KS - 1 - k < 15 ? KS - 1 - k : 15;
+      lgkm_wait<true, younger>(qf[k]);
+      acc = Elem<T>::mfma32(as_vec8<T>(qf[k]), as_vec8<T>(kf[k]), acc);
+    });
+    return acc;
   };
 
-  float mref = neg_inf();    // wave reference m_w (log2 units, wave-uniform)
-  float thr_raw = neg_inf(); // raw score above which m_w must move: (m_w + slack) / sc2
+  float mref = neg_inf();  // wave reference m_w (log2 units, wave-uniform)
+  // sum over the lane's 16 scores of 2^(s sc2 - m_w), those with ok(j)
+  auto exp_sum = [&](const f32x16& s, auto ok) {
+    const float bias = -mref;
+    float e0 = ok(0) ? exp2_fast(fmaf(s[0], sc2, bias)) : 0.f;
+    float e1 = ok(1) ? exp2_fast(fmaf(s[1], sc2, bias)) : 0.f;
+#pragma unroll
+    for (int j = 2; j < 16; j += 2) {
+      e0 += ok(j) ? exp2_fast(fmaf(s[j], sc2, bias)) : 0.f;
+      e1 += ok(j + 1) ? exp2_fast(fmaf(s[j + 1], sc2, bias)) : 0.f;
+    }
+    return e0 + e1;
+  };
+  // raise m_w to the wave's largest score among those with ok(j): rescale
+  // the chunk's running sum and every energy this wave has stored (rare)
+  auto raise = [&](const f32x16& s, auto ok, float& eacc) {
+    float lm = neg_inf();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lm = ok(j) ? fmaxf(lm, s[j]) : lm;
+    const float m_new = wave_max_any(lm) * sc2;
+    const float f = (mref == neg_inf()) ? 0.f : exp2_fast(mref - m_new);
+    eacc *= f;
+    for (int cc = wave; cc < nchunks; cc += 4) {
+      const int bb = cc * 32 + l32;
+      if (hf == 0 && bb < nfv) eb[bb] *= f;
+    }
+    mref = m_new;
+  };
+
   for (int64_t rc = 0; rc < R; rc += kRowsPerPass) {
-    __syncthreads();  // the previous pass is done with the ring and rpos
+    __syncthreads();  // the previous pass is done with qs, qoff and rpos
     if (tid < kRowsPerPass) {
       const int64_t pr = rc + tid;
       int p = -1;
+      int64_t off = -1;
       if (pr < R) {
         const int64_t gg = pr / a.tq;
         p = static_cast<int>(ti.t * a.tq + (pr - gg * a.tq));
+        if (p < a.Lq) off = (ti.h * a.G + gg) * a.q_hs + static_cast<int64_t>(p) * a.q_rs;
       }
       rpos[tid] = p;
+      qoff[tid] = off;
     }
-    // this wave's Q fragments: row rc + 32 wave + l32, data chunks 2k + hf
-    vec8 qf[KS];
-    int my_pos = -1;
+    __syncthreads();
+    // Stage 128 packed rows of Q (zeros past the tile or the valid length),
+    // every load issued before the stores.
     {
-      const int64_t pr = rc + wave * 32 + l32;
-      const uint16_t* qrow = nullptr;
-      if (pr < R) {
-        const int64_t g = pr / a.tq;
-        const int64_t pos = ti.t * a.tq + (pr - g * a.tq);
-        my_pos = static_cast<int>(pos);
-        if (pos < a.Lq) qrow = static_cast<const uint16_t*>(a.q) + (ti.h * a.G + g) * a.q_hs + pos * a.q_rs;
+      constexpr int QN = kRowsPerPass * (D / 8) / kThreads;
+      static_assert(kRowsPerPass * (D / 8) % kThreads == 0, "Q staging splits evenly");
+      u32x4 qst[QN];
+#pragma unroll
+      for (int i = 0; i < QN; ++i) {
+        const int e = tid + i * kThreads;
+        const int r = e / (D / 8);
+        const int64_t off = qoff[r];
+        qst[i] = off >= 0 ? load16(static_cast<const uint16_t*>(a.q) + off + (e - r * (D / 8)) * 8)
+                          : u32x4{0u, 0u, 0u, 0u};
       }
 #pragma unroll
-      for (int k = 0; k < KS; ++k)
-        qf[k] = as_vec8<T>(qrow ? load16(qrow + k * 16 + hf * 8) : u32x4{0u, 0u, 0u, 0u});
+      for (int i = 0; i < QN; ++i) {
+        const int e = tid + i * kThreads;
+        const int r = e / (D / 8);
+        store16(qs + r * LDQ + (e - r * (D / 8)) * 8, qst[i]);
+      }
     }
-    // lowest / highest position of the wave's rows (-1 rows force the checked path)
-    int g_lo = my_pos, g_hi = my_pos;
+    __syncthreads();
+    const int64_t rows_here = (R - rc) < kRowsPerPass ? (R - rc) : kRowsPerPass;
+    const int nrg = static_cast<int>((rows_here + 31) / 32);
+    // per row group (wave-uniform): lowest position, and whether every row
+    // is present and inside the valid length
+    int rg_lo[4];
+    bool rg_full[4];
 #pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
-      g_lo = min(g_lo, __shfl_xor(g_lo, o));
-      g_hi = max(g_hi, __shfl_xor(g_hi, o));
+    for (int rg = 0; rg < 4; ++rg) {
+      int lo = rg < nrg ? rpos[rg * 32 + l32] : -1;
+      int hi = lo;
+#pragma unroll
+      for (int o = 16; o >= 1; o >>= 1) {
+        lo = min(lo, __shfl_xor(lo, o));
+        hi = max(hi, __shfl_xor(hi, o));
+      }
+      rg_lo[rg] = __builtin_amdgcn_readfirstlane(lo);
+      rg_full[rg] = __builtin_amdgcn_readfirstlane(static_cast<int>(lo >= 0 && hi < lq)) != 0;
     }
-#pragma unroll
-    for (int c = 0; c < kAhead; ++c) fill_chunk(c);
 
-    for (int c = 0; c < nchunks; ++c) {
-      vm_wait<GM::NF * (kAhead - 1)>();
-      __syncthreads();  // chunk c in LDS; chunk c-1's stage and partial slot are free
-      fill_chunk(c + kAhead);
-      // S = Q . Kbar^T over the chunk: 8 reads in flight, MFMA k after read k
-      const uint32_t ka = kread + (c % kRing) * GM::TILE;
-      u32x4 kf[KS];
-      StaticFor<0, KS>::run([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        kf[k] = lds_read_b128<true, 0>(ka ^ (32 * k));
+    bool all_full = nrg == 4;
+    int min_lo = rg_lo[0];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      all_full = all_full && rg_full[rg];
+      min_lo = min(min_lo, rg_lo[rg]);
+    }
+    // add the chunk's energies (both halves of the wave) to E_b
+    auto store_chunk = [&](int b, bool b_scored, float eacc) {
+      const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(eacc), __float_as_uint(eacc), false, false);
+      const float etot = __uint_as_float(es[0]) + __uint_as_float(es[1]);
+      if (hf == 0 && b_scored) eb[b] += etot;
+    };
+    // Q fragments of the pass: for D <= 128 every wave keeps all four row
+    // groups in registers (4 x KS x 16 bytes per lane), so the MFMAs read no
+    // LDS; for D = 256 they are read per row group by inline asm (reads
+    // complete in order; each MFMA waits for its own fragment only).
+    u32x4 qr[kResident ? 4 : 1][KS];
+    if constexpr (kResident) {
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) load_q(rg, qr[rg]);
+    }
+    auto rg_scores = [&](auto rgc, const u32x4 (&kf)[KS]) {
+      constexpr int rg = decltype(rgc)::value;
+      if constexpr (kResident) {
+        return mma(qr[rg], kf);
+      } else {
+        u32x4 qf[KS];
+        read_q(rgc, qf);
+        return mma_wait(qf, kf);
+      }
+    };
+    // Fast chunk: every row of the pass sees every scored block.  With
+    // resident Q the MFMAs of row group rg + 1 are interleaved with the sums
+    // of group rg.
+    auto chunk_fast = [&](int c, const u32x4 (&kf)[KS]) {
+      const int b = c * 32 + l32;
+      const bool b_scored = b < nfv;
+      auto ok = [&](int) { return b_scored; };
+      float eacc = 0.f;
+      f32x16 acc0 = rg_scores(std::integral_constant<int, 0>{}, kf), acc1;
+      StaticFor<0, 4>::run([&](auto rgc) {
+        constexpr int rg = decltype(rgc)::value;
+        f32x16& cur = (rg & 1) ? acc1 : acc0;
+        f32x16& nxt = (rg & 1) ? acc0 : acc1;
+        if constexpr (rg + 1 < 4 && kResident) nxt = rg_scores(std::integral_constant<int, rg + 1>{}, kf);
+        float e = exp_sum(cur, ok);
+        if constexpr (rg + 1 < 4 && kResident) {
+#pragma unroll
+          for (int k = 0; k < KS; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 48 / KS, 0);
+          }
+        }
+        if (__ballot(e > kRaiseSum) != 0ull) {
+          raise(cur, ok, eacc);
+          e = exp_sum(cur, ok);
+        }
+        eacc += e;
+        if constexpr (rg + 1 < 4 && !kResident) nxt = rg_scores(std::integral_constant<int, rg + 1>{}, kf);
       });
-      f32x16 acc = {};
-      StaticFor<0, KS>::run([&](auto kc) {
-        constexpr int k = decltype(kc)::value;
-        constexpr int younger = KS - 1 - k < 15 ? KS - 1 - k : 15;
-        lgkm_wait<true, younger>(kf[k]);
-        acc = Elem<T>::mfma32(qf[k], as_vec8<T>(kf[k]), acc);
-      });
-      // the previous chunk's merge runs while the MFMAs are in flight
-      if (c > 0) merge_chunk(c - 1);
-      // Lane holds rows (j/4)*8 + hf*4 + j%4 of the wave's 32 rows, block b.
+      store_chunk(b, b_scored, eacc);
+    };
+    // General chunk: partial passes, rows past the valid length, and blocks
+    // that start after some row of the pass.
+    auto chunk_gen = [&](int c, const u32x4 (&kf)[KS]) {
       const int b = c * 32 + l32;
       const bool b_scored = b < nfv;
       const int lo = max(0, b * bk - offset);
-      float e = 0.f;
-      if (__ballot(!(b_scored && g_lo >= lo && g_hi < lq)) == 0ull) {
-        // every row sees the block: no per-row tests
-        float lm = fmaxf(fmaxf(acc[0], acc[1]), acc[2]);
+      float eacc = 0.f;
+      StaticFor<0, 4>::run([&](auto rgc) {
+        constexpr int rg = decltype(rgc)::value;
+        if (rg < nrg) {
+          const f32x16 s = rg_scores(rgc, kf);
+          bool okr[16];
 #pragma unroll
-        for (int j = 3; j < 15; j += 2) lm = fmaxf(fmaxf(lm, acc[j]), acc[j + 1]);
-        lm = fmaxf(lm, acc[15]);
-        if (__ballot(lm > thr_raw) != 0ull) {  // rare: raise the wave reference
-          mref = wave_max_any(lm) * sc2;
-          thr_raw = (mref + kWaveSlack) / sc2;
+          for (int j = 0; j < 16; ++j) {
+            const int pos = rpos[rg * 32 + (j >> 2) * 8 + hf * 4 + (j & 3)];
+            okr[j] = b_scored && pos >= lo && pos < lq;
+          }
+          auto ok = [&](int j) { return okr[j]; };
+          float e = exp_sum(s, ok);
+          if (__ballot(e > kRaiseSum) != 0ull) {
+            raise(s, ok, eacc);
+            e = exp_sum(s, ok);
+          }
+          eacc += e;
         }
-        const float bias = -mref;
-        float e0 = 0.f, e1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          e0 += exp2_fast(fmaf(acc[j], sc2, bias));
-          e1 += exp2_fast(fmaf(acc[j + 1], sc2, bias));
-        }
-        e = e0 + e1;
-      } else {
-        bool ok[16];
-        float lm = neg_inf();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int pos = rpos[wave * 32 + (j >> 2) * 8 + hf * 4 + (j & 3)];
-          ok[j] = b_scored && pos >= lo && pos < lq;
-          if (ok[j]) lm = fmaxf(lm, acc[j]);
-        }
-        if (__ballot(lm > thr_raw) != 0ull) {
-          mref = wave_max_any(lm) * sc2;
-          thr_raw = (mref + kWaveSlack) / sc2;
-        }
-        const float bias = -mref;
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (ok[j]) e += exp2_fast(fmaf(acc[j], sc2, bias));
+      });
+      store_chunk(b, b_scored, eacc);
+    };
+    auto chunk = [&](int c, const u32x4 (&kf)[KS]) {
+      // lowest position that sees every scored block of the chunk
+      const int lo_last = max(0, min(c * 32 + 31, nfv - 1) * bk - offset);
+      if (all_full && min_lo >= lo_last) chunk_fast(c, kf);
+      else chunk_gen(c, kf);
+    };
+    // this wave's chunks c = wave + 4 i, pooled keys loaded one chunk ahead
+    // where registers allow a second set
+    if constexpr (kPrefetch) {
+      u32x4 ka[KS], kb[KS];
+      load_kbar(wave, ka);
+      for (int c = wave; c < nchunks; c += 8) {
+        load_kbar(c + 4, kb);
+        chunk(c, ka);
+        if (c + 4 >= nchunks) break;
+        load_kbar(c + 8, ka);
+        chunk(c + 4, kb);
       }
-      // partner lane (hf ^ 1) holds the other 16 rows of the block
-      {
-        const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(e), __float_as_uint(e), false, false);
-        e = __uint_as_float(es[0]) + __uint_as_float(es[1]);
+    } else {
+      for (int c = wave; c < nchunks; c += 4) {
+        u32x4 kf[KS];
+        load_kbar(c, kf);
+        chunk(c, kf);
       }
-      if (hf == 0) xe[(c & 1) * 128 + wave * 32 + l32] = e;
-      if (lane == 0) xm[(c & 1) * 4 + wave] = mref;
     }
-    vm_wait<0>();  // the fills past the last chunk
-    __syncthreads();
-    if (nchunks > 0) merge_chunk(nchunks - 1);
+  }
+  // common reference: every wave rescales the blocks it owns by 2^(m_w - G)
+  if (lane == 0) xm[wave] = mref;
+  __syncthreads();
+  const float g = fmaxf(fmaxf(xm[0], xm[1]), fmaxf(xm[2], xm[3]));
+  const float f = (mref == neg_inf()) ? 0.f : exp2_fast(mref - g);
+  for (int cc = wave; cc < nchunks; cc += 4) {
+    const int bb = cc * 32 + l32;
+    if (hf == 0 && bb < nfv) eb[bb] *= f;
   }
   __syncthreads();
-  finish_ring(a, static_cast<int>(ti.h), static_cast<int>(ti.t), static_cast<int>(ti.tile_first),
+  finish_lists(a, static_cast<int>(ti.h), static_cast<int>(ti.t), static_cast<int>(ti.tile_first),
               static_cast<int>(ti.tile_last), nfv, eb, fred, ired);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming path: the hook's path as a persistent kernel.  Each workgroup
+// walks the tiles bid, bid + grid, ... (latest tiles first) in units of
+// StreamGeom::ROWS packed query rows.  A unit's rows are filled into the
+// LDS slot by asynchronous buffer loads (rows padded by one 16-byte
+// granule: conflict-free fragment reads) and copied into registers by every
+// wave, so the MFMAs read registers only.  Wave w owns the 32-block chunks
+// c = w, w + 4, ... of the tile; while the chunks run, the slot holds one
+// pooled-key chunk per wave, filled one chunk ahead (pooled keys are re-read
+// for every tile and the query stream evicts them from L2).  The next
+// unit's Q fill is issued after the chunk loop and lands during the tile's
+// finish, which compacts only the blocks that start inside the causal
+// range (the lists past it are the identity).
+// ---------------------------------------------------------------------------
+template <int D, bool SWZ>
+struct StreamGeom {
+  static constexpr int KS = D / 16;
+  static constexpr int NRG = D <= 128 ? 4 : 2;  // 32-row groups per unit (Q registers: NRG x KS x 16 B)
+  static constexpr int ROWS = NRG * 32;
+  // pooled-key chunk rows: KROWB bytes (a power of two), 16-byte granule g of
+  // row r stored at granule g ^ kswz(r) (conflict-free fragment reads)
+  static constexpr int KROWB = D * 2 <= 128 ? 128 : 256;
+  static constexpr int KG = KROWB / 16;     // granules per row
+  static constexpr int RPI = 1024 / KROWB;  // rows per fill instruction
+  static_assert(!SWZ || D * 2 == KROWB, "swizzled Q rows are exactly one power-of-two row");
+  // Q rows in the slot: SWZ, the pooled-key layout (the host checks that a
+  // fill instruction's rows share one query head and 32-bit row offsets);
+  // otherwise padded by one granule
+  static constexpr int QROWB = SWZ ? KROWB : (D / 8 + 1) * 16;
+  static constexpr int RC = QROWB / 16;     // granules per Q row
+  static constexpr int NF = (ROWS * RC + 4 * 64 - 1) / (4 * 64);  // Q fill instructions per wave
+  static constexpr int SLOT = NF * 4 * 1024 > 4 * 32 * KROWB ? NF * 4 * 1024 : 4 * 32 * KROWB;
+  // registers for the next row group's scores while the sums of one run
+  // (Q NRG x KS x 4 + pooled keys KS x 4 + two accumulators of 16)
+  static constexpr bool PIPE = NRG * KS * 4 + KS * 4 + 32 <= 160;
+  // one pooled-key chunk per wave in the Q slot, which is idle while the
+  // chunks run
+  static constexpr int KSLOT = 32 * KROWB;
+  static constexpr int NFK = KSLOT / 1024;  // fill instructions per chunk
+  static_assert(4 * KSLOT <= SLOT, "four pooled-key slots fit in the Q slot");
+  static __device__ __forceinline__ int kswz(int row) { return KG == 16 ? (row & 15) : ((row >> 1) & 7); }
+  // kswz(RPI j + lr) = swz_inst(j) ^ swz_lane(lr) for lr < RPI (disjoint bits)
+  static constexpr int swz_inst(int j) { return KG == 16 ? 4 * (j & 3) : 4 * (j & 1); }
+  static __device__ __forceinline__ uint32_t swz_lane(uint32_t lr) { return KG == 16 ? lr : (lr >> 1); }
+};
+
+// dynamic LDS (the Q slot is a separate static array, so that the
+// compiler's wait for the asynchronous fills covers reads of the slot only):
+// E_b[Nb], row positions [256], wave references [4], wave maxima [4],
+// list counts [8]
+constexpr size_t stream_lds_bytes(int64_t Nb) { return static_cast<size_t>(Nb) * 4 + (256 + 4 + 4 + 8) * 4; }
+
+template <typename T, int D, bool SWZ>
+__global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(1, 2))) void select_stream_kernel(
+    SelectArgs a) {
+  using SG = StreamGeom<D, SWZ>;
+  constexpr int KS = SG::KS;
+  constexpr int NRG = SG::NRG;
+  constexpr int ROWS = SG::ROWS;
+  constexpr int RC = SG::RC;
+  __shared__ __align__(1024) unsigned char qslot[SG::SLOT];
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int Nb = static_cast<int>(a.Nb);
+  float* eb = reinterpret_cast<float*>(smem);      // block energies against the owner's m_w
+  int* rpos = reinterpret_cast<int*>(eb + Nb);     // [ROWS] unit row -> position, -1: no such row
+  float* xm = reinterpret_cast<float*>(rpos + 256);  // [4] wave references m_w
+  float* wmx = xm + 4;                             // [4] wave maxima of E_b
+  int* ired = reinterpret_cast<int*>(wmx + 4);     // [8] list counts
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hf = lane >> 5;
+  const int Hkv = static_cast<int>(a.Hkv);
+  const int Nt = static_cast<int>(a.Nt);
+  const int tq = static_cast<int>(a.tq);
+  const int R = static_cast<int>(a.G * a.tq);
+  const int npass = (R + ROWS - 1) / ROWS;
+  const int lq = static_cast<int>(a.Lq);
+  const int offset = static_cast<int>(a.offset);
+  const int bk = static_cast<int>(a.bk);
+  const float sc2 = a.scale * kLog2e;  // > 0 on this path
+  const int total = Hkv * Nt;
+  const uint32_t tq_magic = a.tq_magic;
+  // pr / tq for pr * tq < 2^32 (host-checked): multiply by ceil(2^32 / tq)
+  auto div_tq = [&](int pr) { return static_cast<int>(__umulhi(static_cast<uint32_t>(pr), tq_magic)); };
+
+  // ---- fills: fill instruction i of this wave writes LDS granules
+  // [64 (4 i + wave), 64 (4 i + wave + 1)) of the slot; granule p holds row
+  // p / RC, data granule p % RC (the last granule of a row is padding) ----
+  // Arguments used once per tile are read again from the argument segment
+  // (scalar cache) through a pointer the compiler cannot hoist: kept in
+  // registers across the persistent loop they would exhaust the SGPRs.
+  typedef __attribute__((address_space(4))) const SelectArgs* kernarg_args;
+  auto fresh = [&]() {
+    // the kernel's only argument sits at the start of its argument segment
+    kernarg_args p = (kernarg_args)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return p;
+  };
+  // Workgroup barrier that leaves the asynchronous Q fill in flight: only
+  // this kernel's LDS writes (ds_*) must be visible across it, and nothing
+  // reads the Q slot before the next vm_wait<0> + __syncthreads.  (A plain
+  // __syncthreads would also wait for the fill.)
+  auto barrier_lds = []() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+  auto issue_fill = [&](int tile_i, int pass) {
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    kernarg_args f = fresh();
+    const int h = tile_i % Hkv;
+    const int t = Nt - 1 - tile_i / Hkv;
+    const uint32_t q_hs = static_cast<uint32_t>(f->q_hs), q_rs = static_cast<uint32_t>(f->q_rs);
+    const uint32_t q_bytes = static_cast<uint32_t>(((f->G - 1) * f->q_hs + (f->Lq - 1) * f->q_rs + D) * 2);
+    const rsrc_t qr = make_rsrc(static_cast<const uint16_t*>(f->q) + h * f->G * f->q_hs, q_bytes);
+    // recomputed per call rather than kept live through the chunk loop
+    uint32_t ln = static_cast<uint32_t>(lane);
+    asm volatile("" : "+v"(ln));
+    if constexpr (SWZ) {
+      // instruction j = 4 i + wave fills rows RPI j + lr (lr = lane / KG), all
+      // of one query head: scalar row offsets, granule (lane % KG) ^ kswz
+      const uint32_t lr = ln / SG::KG;
+      const uint32_t lanepart = lr * q_rs * 2u + 16u * ((ln % SG::KG) ^ SG::swz_lane(lr));
+#pragma unroll
+      for (int i = 0; i < SG::NF; ++i) {
+        const int j = i * 4 + wave;
+        const int pr0 = pass * ROWS + j * SG::RPI;
+        const int g = div_tq(pr0);
+        const int pos0 = t * tq + pr0 - g * tq;
+        const uint32_t sbase = (static_cast<uint32_t>(g) * q_hs + static_cast<uint32_t>(pos0) * q_rs) * 2u;
+        // the scalar offset stays uniform (sbase < 2^31): an invalid lane's
+        // kOOB + sbase is still past the range and reads zeros
+        const bool ok = (j * SG::RPI < ROWS) & (pr0 < R) & (static_cast<int>(lr) < lq - pos0);
+        const uint32_t voff = ok ? (lanepart ^ (16u * SG::swz_inst(j))) : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_ptr)(qslot + j * 1024), 16, voff, sbase, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < SG::NF; ++i) {
+        const int p = (i * 4 + wave) * 64 + static_cast<int>(ln);
+        const int row = p / RC;
+        const int gr = p - row * RC;
+        const int pr = pass * ROWS + row;
+        const int g = div_tq(pr);
+        const int pos = t * tq + pr - g * tq;
+        const bool ok = (row < ROWS) & (gr < D / 8) & (pr < R) & (pos < lq);
+        const uint32_t off = ok ? (g * q_hs + pos * q_rs + gr * 8) * 2 : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qr, (lds_ptr)(qslot + (i * 4 + wave) * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+
+  // Pooled keys of chunk c into this wave's slot: fill instruction i, lane
+  // -> slot granule p = 64 i + lane, row p / KG, holding data granule
+  // (p % KG) ^ kswz(row) of block c*32 + row.  Blocks past nfv may hold any
+  // in-range data (their scores are masked); padding granules of D = 96
+  // and blocks past Nb load zeros.
+  unsigned char* const kslot = qslot + wave * SG::KSLOT;
+  auto fill_kbar = [&](const rsrc_t& pkr, int c) {
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    uint32_t ln = static_cast<uint32_t>(lane);  // recomputed per call rather than kept live
+    asm volatile("" : "+v"(ln));
+    const uint32_t cbase = static_cast<uint32_t>(c) * 32u * D * 2u;
+    if constexpr (SWZ) {
+      // instruction i fills rows RPI i + lr (lr = lane / KG): byte
+      // (RPI i + lr) KROWB + 16 ((lane % KG) ^ kswz(row)) of the chunk
+      const uint32_t lr = ln / SG::KG;
+      const uint32_t lanepart = lr * SG::KROWB + 16u * ((ln % SG::KG) ^ SG::swz_lane(lr));
+#pragma unroll
+      for (int i = 0; i < SG::NFK; ++i) {
+        const uint32_t voff = lanepart ^ (16u * SG::swz_inst(i));
+        const uint32_t soff = cbase + i * 1024u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(kslot + i * 1024), 16, voff, soff, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < SG::NFK; ++i) {
+        const uint32_t row = (i * 64u + ln) / SG::KG;
+        const uint32_t gr = ((i * 64u + ln) % SG::KG) ^ static_cast<uint32_t>(SG::kswz(static_cast<int>(row)));
+        const uint32_t off = gr < D / 8 ? cbase + (row * D + gr * 8u) * 2u : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(pkr, (lds_ptr)(kslot + i * 1024), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  // fragment k of the chunk in the slot: block row l32, data granule
+  // 2k + hf, i.e. byte (2k + hf) ^ kswz(l32) of the row: the k-dependent
+  // part is an XOR of 32 k on a row-aligned base
+  const uint32_t kread = lds_addr(kslot) + l32 * SG::KROWB + ((16 * hf) ^ (16 * SG::kswz(l32)));
+  auto read_kbar = [&](u32x4 (&kf)[KS]) {
+    typedef __attribute__((address_space(3))) const u32x4* lds_u32x4p;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) kf[k] = *(lds_u32x4p)(static_cast<uintptr_t>(kread ^ (32 * k)));
+  };
+  auto mma = [&](const u32x4 (&qf)[KS], const u32x4 (&kf)[KS]) {
+    f32x16 acc = {};
+#pragma unroll
+    for (int k = 0; k < KS; ++k) acc = Elem<T>::mfma32(as_vec8<T>(qf[k]), as_vec8<T>(kf[k]), acc);
+    return acc;
+  };
+
+  float mref = neg_inf();  // wave reference m_w (log2 units, wave-uniform)
+  // sum over the lane's 16 scores of 2^(s sc2 - m_w), those with ok(j)
+  auto exp_sum = [&](const f32x16& s, auto ok) {
+    const float bias = -mref;
+    float e0 = ok(0) ? exp2_fast(fmaf(s[0], sc2, bias)) : 0.f;
+    float e1 = ok(1) ? exp2_fast(fmaf(s[1], sc2, bias)) : 0.f;
+#pragma unroll
+    for (int j = 2; j < 16; j += 2) {
+      e0 += ok(j) ? exp2_fast(fmaf(s[j], sc2, bias)) : 0.f;
+      e1 += ok(j + 1) ? exp2_fast(fmaf(s[j + 1], sc2, bias)) : 0.f;
+    }
+    return e0 + e1;
+  };
+
+  if (static_cast<int>(blockIdx.x) >= total) return;
+  issue_fill(blockIdx.x, 0);
+  for (int tile_i = blockIdx.x; tile_i < total; tile_i += gridDim.x) {
+    const int h = tile_i % Hkv;
+    const int t = Nt - 1 - tile_i / Hkv;  // latest tiles (longest rows) first
+    const int tile_first = offset + t * tq;
+    const int tile_last = min(tile_first + tq, offset + lq) - 1;
+    const int nfv = min(Nb, max(0, (tile_last + 1) / bk));  // blocks that end inside the causal range
+    const int nchunks = (nfv + 31) / 32;
+    kernarg_args ta = fresh();
+    const rsrc_t pkr = make_rsrc(static_cast<const uint16_t*>(ta->pk) + static_cast<int64_t>(h) * ta->pk_hs,
+                                 static_cast<uint32_t>(Nb * D * 2));
+    mref = neg_inf();
+    float emax_w = 0.f;  // largest E_b of this wave's blocks (last pass)
+
+    for (int pass = 0; pass < npass; ++pass) {
+      vm_wait<0>();
+      __syncthreads();  // the unit's fill has landed; the previous unit and finish are done with LDS
+      if (tid < ROWS) {
+        const int pr = pass * ROWS + tid;
+        rpos[tid] = pr < R ? t * tq + pr - div_tq(pr) * tq : -1;
+      }
+      // the unit's Q fragments: row rg*32 + l32, data granules 2k + hf
+      u32x4 qr[NRG][KS];
+      if constexpr (SWZ) {
+        // kswz(rg*32 + l32) = kswz(l32): the same XOR pattern as the pooled keys
+        typedef __attribute__((address_space(3))) const u32x4* lds_u32x4p;
+        const uint32_t qread = lds_addr(qslot) + l32 * SG::QROWB + ((16 * hf) ^ (16 * SG::kswz(l32)));
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+          for (int k = 0; k < KS; ++k)
+            qr[rg][k] = *(lds_u32x4p)(static_cast<uintptr_t>((qread ^ (32 * k)) + rg * 32 * SG::QROWB));
+      } else {
+#pragma unroll
+        for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+          for (int k = 0; k < KS; ++k)
+            qr[rg][k] = *reinterpret_cast<const u32x4*>(qslot + ((rg * 32 + l32) * RC + 2 * k + hf) * 16);
+      }
+      __syncthreads();  // rpos written; every wave holds its Q, so the slot may be refilled
+      // per row group (wave-uniform): lowest position, and whether every
+      // row is present and inside the valid length
+      const int nrg = (min(R - pass * ROWS, ROWS) + 31) / 32;
+      bool all_full = nrg == NRG;
+      int min_lo = 0x7fffffff;
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg) {
+        int lo = rpos[rg * 32 + l32];
+        int hi = lo;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+          lo = min(lo, __shfl_xor(lo, o));
+          hi = max(hi, __shfl_xor(hi, o));
+        }
+        lo = __builtin_amdgcn_readfirstlane(lo);
+        hi = __builtin_amdgcn_readfirstlane(hi);
+        all_full = all_full && lo >= 0 && hi < lq;
+        min_lo = min(min_lo, lo);
+      }
+
+      // raise m_w to the wave's largest score among those with ok(j):
+      // rescale the running sums and every energy this wave has stored
+      // (rare; entries of chunks not yet stored in the first pass are stale
+      // and will be overwritten)
+      auto raise = [&](const f32x16& s, auto ok, float& eacc) {
+        float lm = neg_inf();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) lm = ok(j) ? fmaxf(lm, s[j]) : lm;
+        const float m_new = wave_max_dpp(lm) * sc2;
+        const float f = (mref == neg_inf()) ? 0.f : exp2_fast(mref - m_new);
+        eacc *= f;
+        emax_w *= f;
+        for (int cc = wave; cc < nchunks; cc += 4) {
+          const int bb = cc * 32 + l32;
+          if (hf == 0 && bb < nfv) eb[bb] *= f;
+        }
+        mref = m_new;
+      };
+      // add the chunk's energies (both halves of the wave) to E_b
+      auto store_chunk = [&](int b, bool b_scored, float eacc) {
+        const auto es = __builtin_amdgcn_permlane32_swap(__float_as_uint(eacc), __float_as_uint(eacc), false, false);
+        float etot = __uint_as_float(es[0]) + __uint_as_float(es[1]);
+        if (hf == 0 && b_scored) {
+          if (pass > 0) etot += eb[b];
+          eb[b] = etot;
+        }
+        if (pass == npass - 1 && b_scored) emax_w = fmaxf(emax_w, etot);
+      };
+      // this wave's chunks c = wave + 4 i: chunk c + 4 is filled into the
+      // slot while chunk c runs from registers
+      if (wave < nchunks) fill_kbar(pkr, wave);
+      for (int c = wave; c < nchunks; c += 4) {
+        u32x4 kf[KS];
+        vm_wait<0>();
+        read_kbar(kf);
+        if (c + 4 < nchunks) {
+          // the slot's reads must complete before the fill overwrites it
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          fill_kbar(pkr, c + 4);
+        }
+        const int b = c * 32 + l32;
+        const bool b_scored = b < nfv;
+        float eacc = 0.f;
+        // lowest position that sees every scored block of the chunk
+        const int lo_last = max(0, min(c * 32 + 31, nfv - 1) * bk - offset);
+        if (all_full && min_lo >= lo_last) {
+          // every row of the unit sees every scored block; the MFMAs of row
+          // group rg + 1 are interleaved with the sums of group rg
+          auto ok = [&](int) { return b_scored; };
+          f32x16 acc0 = mma(qr[0], kf), acc1;
+          StaticFor<0, NRG>::run([&](auto rgc) {
+            constexpr int rg = decltype(rgc)::value;
+            f32x16& cur = (rg & 1) ? acc1 : acc0;
+            f32x16& nxt = (rg & 1) ? acc0 : acc1;
+            if constexpr (rg + 1 < NRG && SG::PIPE) nxt = mma(qr[rg + 1], kf);
+            float e = exp_sum(cur, ok);
+            if constexpr (rg + 1 < NRG && SG::PIPE) {
+#pragma unroll
+              for (int k = 0; k < KS; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 48 / KS, 0);
+              }
+            }
+            if (__ballot(e > kRaiseSum) != 0ull) {
+              raise(cur, ok, eacc);
+              e = exp_sum(cur, ok);
+            }
+            eacc += e;
+            if constexpr (rg + 1 < NRG && !SG::PIPE) nxt = mma(qr[rg + 1], kf);
+          });
+        } else {
+          // partial units, rows past the valid length, blocks that start
+          // after some row of the unit: each score is tested
+          const int lo = max(0, b * bk - offset);
+          StaticFor<0, NRG>::run([&](auto rgc) {
+            constexpr int rg = decltype(rgc)::value;
+            if (rg < nrg) {
+              const f32x16 sc = mma(qr[rg], kf);
+              auto ok = [&](int j) {
+                const int pos = rpos[rg * 32 + (j >> 2) * 8 + hf * 4 + (j & 3)];
+                return b_scored && pos >= lo && pos < lq;
+              };
+              float e = exp_sum(sc, ok);
+              if (__ballot(e > kRaiseSum) != 0ull) {
+                raise(sc, ok, eacc);
+                e = exp_sum(sc, ok);
+              }
+              eacc += e;
+            }
+          });
+        }
+        store_chunk(b, b_scored, eacc);
+      }
+      if (pass + 1 < npass) {
+        __syncthreads();  // every wave is done with its pooled-key slot
+        issue_fill(tile_i, pass + 1);
+      }
+    }
+
+    // ---- finish (selection.py:183-195, kernel.py:141-184) ----
+    const float wm = wave_max_dpp(emax_w);
+    if (lane == 0) {
+      xm[wave] = mref;
+      wmx[wave] = wm;
+    }
+    __syncthreads();  // xm, wmx written; every wave is done with its pooled-key slot
+    if (tile_i + static_cast<int>(gridDim.x) < total) issue_fill(tile_i + gridDim.x, 0);  // lands during the finish
+    // E_b = eb[b] 2^(m_w - G) with w the owner of b and G = max m_w
+    const float g = fmaxf(fmaxf(xm[0], xm[1]), fmaxf(xm[2], xm[3]));
+    float fw[4], emax = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      fw[w] = (xm[w] == neg_inf()) ? 0.f : exp2_fast(xm[w] - g);
+      emax = fmaxf(emax, wmx[w] * fw[w]);
+    }
+    kernarg_args fa = fresh();
+    const float thr = fa->alpha * emax;
+    const int nvis = min(Nb, tile_last / bk + 1);  // blocks that start inside the causal range
+    const int sink = static_cast<int>(fa->sink);
+    const int first_minus_window = tile_first - static_cast<int>(fa->window);
+    const int lk = static_cast<int>(fa->Lk);
+    const bool tail = t >= Nt - static_cast<int>(fa->last_n);
+    // branch-free: every lane reads an E_b (clamped index; entries past
+    // nfv are discarded), so no LDS read is left pending in a branch
+    auto flags = [&](int b, bool& sel, bool& pru) {
+      const float e_raw = eb[min(b, Nb - 1)];
+      const int w = (b >> 5) & 3;
+      const float f = w == 0 ? fw[0] : (w == 1 ? fw[1] : (w == 2 ? fw[2] : fw[3]));
+      const float E = b < nfv ? e_raw * f : 0.f;
+      const int bs = b * bk;
+      const int be = bs + bk;
+      const bool forced = bs < sink || be > first_minus_window || tail;
+      sel = (E >= thr || forced) && bs <= tile_last;
+      pru = !sel && min(be, lk) <= tile_first;
+    };
+    const int span = ((nvis + 4 * 64 - 1) / (4 * 64)) * 64;
+    const int w0 = min(nvis, wave * span), w1 = min(nvis, w0 + span);
+    // flags evaluated once: bit it of selbits / prubits is the lane's block
+    // of iteration it (span <= FPV2_MAX_BLOCKS / 4: at most 32 iterations)
+    static_assert(FPV2_MAX_BLOCKS <= 4 * 64 * 32, "finish flags fit 32 bits per lane");
+    int ns = 0, np = 0;
+    uint32_t selbits = 0, prubits = 0;
+    for (int base = w0, it = 0; base < w1; base += 64, ++it) {
+      const int b = base + lane;
+      bool sel, pru;
+      flags(b, sel, pru);
+      sel = sel && b < w1;
+      pru = pru && b < w1;
+      selbits |= static_cast<uint32_t>(sel) << it;
+      prubits |= static_cast<uint32_t>(pru) << it;
+      ns += __popcll(__ballot(sel));
+      np += __popcll(__ballot(pru));
+    }
+    if (lane == 0) {
+      ired[wave] = ns;
+      ired[4 + wave] = np;
+    }
+    barrier_lds();
+    int run_s = 0, run_p = 0, tot_s = 0, tot_p = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int cs = ired[w], cp = ired[4 + w];
+      run_s += w < wave ? cs : 0;
+      run_p += w < wave ? cp : 0;
+      tot_s += cs;
+      tot_p += cp;
+    }
+    const int64_t row = static_cast<int64_t>(h) * Nt + t;
+    typedef __attribute__((address_space(1))) int32_t g_i32;
+    typedef __attribute__((address_space(1))) uint8_t g_u8;
+    g_i32* ids = (g_i32*)(fa->ids + row * Nb);
+    g_i32* pids = (g_i32*)(fa->pids + row * Nb);
+    g_u8* selo = fa->sel_out ? (g_u8*)(fa->sel_out + row * Nb) : nullptr;
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = w0, it = 0; base < w1; base += 64, ++it) {
+      const int b = base + lane;
+      const bool sel = (selbits >> it) & 1u;
+      const bool pru = (prubits >> it) & 1u;
+      const uint64_t ms = __ballot(sel);
+      const uint64_t mp = __ballot(pru);
+      if (b < w1) {
+        const int ps = run_s + __popcll(ms & below);  // selected before b
+        const int pp = run_p + __popcll(mp & below);
+        ids[sel ? ps : tot_s + (b - ps)] = b;
+        pids[pru ? pp : tot_p + (b - pp)] = b;
+        if (selo) selo[b] = sel;
+      }
+      run_s += __popcll(ms);
+      run_p += __popcll(mp);
+    }
+    // blocks that start past the tile: neither selected nor pruned (the
+    // host routes key lengths that do not cover the queries elsewhere)
+    for (int b = nvis + tid; b < Nb; b += kThreads) {
+      ids[b] = b;
+      pids[b] = b;
+      if (selo) selo[b] = 0;
+    }
+    if (tid == 0) {
+      ((g_i32*)fa->counts)[row] = tot_s;
+      ((g_i32*)fa->pcounts)[row] = tot_p;
+    }
+  }
+  vm_wait<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -870,6 +1451,20 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(CompactArgs a) {
   }
 }
 
+// compute units of the current device (the streaming grid is two
+// workgroups per unit)
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <typename K>
 int launch_with_lds(K kernel, dim3 grid, size_t lds, hipStream_t stream, const SelectArgs& a) {
   if (lds > 160 * 1024) return fail(FPV2_ERR_UNSUPPORTED, "score_select: %zu bytes of LDS exceed 160 KiB", lds);
@@ -895,15 +1490,43 @@ int launch_generic(K kernel, dim3 grid, size_t lds, hipStream_t stream, const Se
 template <typename T>
 int dispatch_mfma(int64_t D, dim3 grid, hipStream_t stream, const SelectArgs& a, bool* done) {
   *done = true;
-  // the ring kernel keeps key positions and list entries in 32 bits
+  // the hook's paths keep key positions and list entries in 32 bits
   const bool small = a.Nb * a.bk <= (1LL << 30) && a.offset + a.Lq_pad <= (1LL << 30) &&
                      a.sink <= (1LL << 30) && a.window <= (1LL << 30) && a.Nt <= (1LL << 30);
+  // streaming kernel: 32-bit query offsets within one KV head's rows, exact
+  // 32-bit division by tq, and key lengths that cover every query
+  const int64_t q_span = (a.G - 1) * a.q_hs + (a.Lq - 1) * a.q_rs + D;
+  const bool stream_ok = small && a.tq >= 2 && (a.G * a.tq + 256) * a.tq < (1LL << 32) &&
+                         q_span * 2 < kMaxRsrcBytes && a.Nb * D * 2 < kMaxRsrcBytes &&
+                         a.Lk > a.offset + (a.Nt - 1) * a.tq && a.Hkv * a.Nt < (1LL << 31);
+  if (a.scores == nullptr && a.scale > 0.f && a.ids != nullptr && stream_ok) {
+    SelectArgs s = a;
+    s.tq_magic = static_cast<uint32_t>(((1ull << 32) + static_cast<uint64_t>(a.tq) - 1) / static_cast<uint64_t>(a.tq));
+    const int64_t tiles = a.Hkv * a.Nt;
+    const dim3 sgrid(static_cast<unsigned>(tiles < 2LL * cu_count() ? tiles : 2LL * cu_count()));
+    // swizzled Q rows: a fill instruction's RPI rows belong to one query
+    // head (tq, R multiples of RPI) and their row offsets keep the granule
+    // bits clear (q_rs * 2 a multiple of the row size)
+    const int64_t rpi = 1024 / (D * 2);
+    const bool swz = (D == 64 || D == 128) && a.tq % rpi == 0 && (a.q_rs * 2) % (D * 2) == 0;
+    switch (D) {
+      case 64:
+        return swz ? launch_with_lds(select_stream_kernel<T, 64, true>, sgrid, stream_lds_bytes(a.Nb), stream, s)
+                   : launch_with_lds(select_stream_kernel<T, 64, false>, sgrid, stream_lds_bytes(a.Nb), stream, s);
+      case 96: return launch_with_lds(select_stream_kernel<T, 96, false>, sgrid, stream_lds_bytes(a.Nb), stream, s);
+      case 128:
+        return swz ? launch_with_lds(select_stream_kernel<T, 128, true>, sgrid, stream_lds_bytes(a.Nb), stream, s)
+                   : launch_with_lds(select_stream_kernel<T, 128, false>, sgrid, stream_lds_bytes(a.Nb), stream, s);
+      default: break;  // D = 256: the owner path below (its registers hold no resident Q)
+    }
+  }
   if (a.scores == nullptr && a.scale > 0.f && a.ids != nullptr && small) {
     switch (D) {
-      case 64: return launch_with_lds(select_ring_kernel<T, 64>, grid, ring_lds_bytes<64>(a.Nb), stream, a);
-      case 96: return launch_with_lds(select_ring_kernel<T, 96>, grid, ring_lds_bytes<96>(a.Nb), stream, a);
-      case 128: return launch_with_lds(select_ring_kernel<T, 128>, grid, ring_lds_bytes<128>(a.Nb), stream, a);
-      case 256: return launch_with_lds(select_ring_kernel<T, 256>, grid, ring_lds_bytes<256>(a.Nb), stream, a);
+      case 64: return launch_with_lds(select_own_kernel<T, 64>, grid, own_lds_bytes<64>(a.Nb), stream, a);
+      case 96: return launch_with_lds(select_own_kernel<T, 96>, grid, own_lds_bytes<96>(a.Nb), stream, a);
+      case 128: return launch_with_lds(select_own_kernel<T, 128>, grid, own_lds_bytes<128>(a.Nb), stream, a);
+      case 256: return launch_with_lds(select_own_kernel<T, 256>, grid, own_lds_bytes<256>(a.Nb), stream, a);
+
       default: break;
     }
   }

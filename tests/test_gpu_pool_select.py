@@ -167,10 +167,9 @@ def test_selection_and_scores_match_oracle(cuda, dtype, head_dim, offset, qlen):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
 @pytest.mark.parametrize("offset,qlen,tile_q", [(0, 512, 16), (77, 300, 16), (40, 700, 64)])
-def test_ring_selection_matches_oracle(cuda, dtype, head_dim, offset, qlen, tile_q):
-    # Without a score output the selection runs the LDS-ring kernel (row groups
-    # per wave, pooled-key chunks shared through LDS).  tile_q = 64 gives 256
-    # packed rows per tile: two 128-row passes over the ring.
+def test_mask_only_selection_matches_oracle(cuda, dtype, head_dim, offset, qlen, tile_q):
+    # A mask without lists and without scores runs the score-output kernel's
+    # selection.  tile_q = 64 gives 256 packed rows per tile (two passes).
     config = FPV2Config(block_k=32, tile_q=tile_q, alpha=0.2, sink_tokens=32, window_tokens=64,
                         last_n_blocks=1, score_chunk_tiles=4)
     q, k, _ = structured_qkv(length=offset + qlen + 100, query_heads=8, kv_heads=2,
@@ -286,6 +285,44 @@ def test_fused_selection_lists_match_oracle(cuda, seq, planted):
     if not near.any():
         want_o = orc.compact_block_indices(sel_o, config=_cfg(cfg), offset=offset,
                                            query_length=seq, key_length=seq)
+        for g, w in zip(lists, want_o):
+            assert np.array_equal(to_np(g), w)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+@pytest.mark.parametrize("lq,lk,tile_q", [(512, 512, 16), (300, 377, 16), (700, 740, 64), (300, 300, 6)])
+def test_hook_lists_match_oracle(cuda, dtype, head_dim, lq, lk, tile_q):
+    # Lists requested, no score output: the hook's selection.  head_dim <= 128
+    # runs the streaming kernel (swizzled Q rows when tile_q is a multiple of
+    # a fill's rows, padded rows for tile_q = 6 and head_dim 96; tile_q = 64
+    # gives two 128-row units per tile), head_dim 256 the owner kernel.
+    config = FPV2Config(block_k=32, tile_q=tile_q, alpha=0.2, sink_tokens=32, window_tokens=64,
+                        last_n_blocks=1)
+    q_all, k, _ = structured_qkv(length=lk, query_heads=8, kv_heads=2, head_dim=head_dim,
+                                 block_size=32, seed=head_dim + lq + tile_q, dtype=dtype)
+    q = q_all[:, lk - lq:].contiguous()
+    cfg, offset, pk, mask, lists = _hook_select(q.to(cuda), k.to(cuda), config, total_tokens=lk)
+    assert offset == lk - lq
+    lq_pad = -(-lq // tile_q) * tile_q
+    nb = pk.shape[1]
+    qp = torch.zeros((8, lq_pad, head_dim), dtype=dtype)
+    qp[:, :lq] = q
+    kp = torch.zeros((2, nb * 32, head_dim), dtype=dtype)
+    kp[:, :lk] = k
+    pk_o = orc.pool_blocks(to_np(kp), 32, out_dtype=_DT[dtype])
+    assert np.array_equal(to_np(pk), pk_o)
+    sel_o, _, ratio = orc.block_scores_and_select(
+        to_np(qp), pk_o, scale=head_dim ** -0.5, config=_cfg(cfg), offset=offset,
+        query_length=lq, return_ratio=True)
+    near = _assert_selection_parity(to_np(mask), sel_o, ratio, config.alpha)
+    want = orc.compact_block_indices(to_np(mask).astype(bool), config=_cfg(cfg), offset=offset,
+                                     query_length=lq, key_length=lk)
+    for g, w in zip(lists, want):
+        assert np.array_equal(to_np(g), w)
+    if not near.any():
+        want_o = orc.compact_block_indices(sel_o, config=_cfg(cfg), offset=offset,
+                                           query_length=lq, key_length=lk)
         for g, w in zip(lists, want_o):
             assert np.array_equal(to_np(g), w)
 
