@@ -140,6 +140,16 @@ struct AttnArgs {
   uint32_t q_bytes, k_bytes, v_bytes, pooled_bytes;  // descriptor ranges
 };
 
+// Workgroup barrier for data written to LDS by ds_write: it waits for this
+// wave's LDS operations only.  __syncthreads() also waits for every
+// outstanding global load, here the fills of the ring stages ahead.
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <typename V>
+__device__ __forceinline__ V pick(bool c, V x, V y) {
+  return c ? x : y;
+}
 __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
@@ -369,10 +379,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // Fill instruction i of this wave covers rows [jj*RPI, (jj+1)*RPI) of the K
   // (i < NIK) or V sub-tile, jj = wave + (i % NIK) * WAVES; lane -> chunk
   // lane % RC of row jj*RPI + lane / RC, holding data chunk c = that ^ mask.
-  const rsrc_t kr = make_rsrc(a.k + h * a.k_hs, a.k_bytes);
-  const rsrc_t vr = make_rsrc(a.v + h * a.v_hs, a.v_bytes);
-  const rsrc_t pkr = make_rsrc(a.pk + h * a.pooled_hs, a.pooled_bytes);
-  const rsrc_t pvr = make_rsrc(a.pv + h * a.pooled_hs, a.pooled_bytes);
+  const uint16_t* const kh = a.k + h * a.k_hs;
+  const uint16_t* const vh = a.v + h * a.v_hs;
+  const uint16_t* const pkh = a.pk + h * a.pooled_hs;
+  const uint16_t* const pvh = a.pv + h * a.pooled_hs;
   auto fill_row = [&](int i, int ln) { return (wave + (i % NIK) * WAVES) * GM::RPI + ln / GM::RC; };
   auto fill_chunk = [&](int i, int row, int ln) {
     return (ln % GM::RC) ^ (i < NIK ? GM::kmask(row) : GM::vmask(row));
@@ -396,17 +406,24 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     pre[i] = c < GM::DG ? (row * rs + c * 8) * 2 : -1;
   }
   const uint32_t smem_lds = lds_addr(smem);
-  // Correction fills take their pooled rows' block ids from cid: the pruned
-  // list entries li + fill_row(j, lane) of the next correction step (li),
-  // loaded one step ahead (the first step's here), so that no fill address
-  // waits on a load or a lane exchange.
+  // Correction fills take their pooled rows' block ids from cid: the
+  // pruned-list entries li + fill_row(j, lane) of the next correction step
+  // (the first one's, loaded at set-up, through the exact phase).  A
+  // correction fill computes its addresses from cid, then loads the next
+  // step's entries into cid, then issues its fills.  The fills of every kind
+  // of step are issued on one path after that point: the compiler's wait
+  // analysis does not tell branches apart, and a load that some path does
+  // not follow with the step's fills (or that is consumed at once) gets a
+  // vmcnt(0) wait before its use, draining every fill in flight.  Followed
+  // by the fills, the loads are known to be complete after the fills_done()
+  // wait before their use.  Raw buffer loads over the rest of the list row:
+  // entries past the row read as 0; values are clamped where they are used.
   int cid[NIK];
   auto load_cids = [&](int li) {
+    const rsrc_t pr = make_rsrc(pids + li, static_cast<uint32_t>(max(Nb - li, 0)) * 4u);
 #pragma unroll
-    for (int j = 0; j < NIK; ++j) {
-      const int e = li + fill_row(j, lane);
-      cid[j] = (CORR && e < pr_count) ? clampi(pids[e], 0, Nb - 1) : 0;
-    }
+    for (int j = 0; j < NIK; ++j)
+      cid[j] = CORR ? static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(pr, fill_row(j, lane) * 4, 0, 0)) : 0;
   };
   load_cids(0);
   auto fill_step = [&](const Step& s, int stage) {
@@ -414,7 +431,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     // (a lambda returning an LDS pointer would drop the kernel from the host
     // pass, so the destination is spelled out at each fill)
     uint8_t* const sp = smem + stage * GM::STAGE;
-    if (!s.corr) {
+    // (uniform: it selects the fills' buffer descriptors below)
+    const bool corr = CORR && __builtin_amdgcn_readfirstlane(s.corr) != 0;
+    uint32_t off[NI];
+    if (!corr) {
       const uint32_t kb = static_cast<uint32_t>(s.key0 * a.k_rs * 2);
       const uint32_t vb = static_cast<uint32_t>(s.key0 * a.v_rs * 2);
       if (s.nkeys == BN) {  // full sub-tile
@@ -422,10 +442,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
         for (int i = 0; i < NI; ++i) {
           bool ok = true;
           if constexpr (GM::DG < GM::RC) ok = pre[i] >= 0;
-          const uint32_t off = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              i < NIK ? kr : vr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
-              16, off, 0, 0, 0);
+          off[i] = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
         }
       } else {  // partial (end of the keys or of a block) or empty
         const int ln = opaque_lane();
@@ -433,10 +450,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
         for (int i = 0; i < NI; ++i) {
           bool ok = fill_row(i, ln) < s.nkeys;
           if constexpr (GM::DG < GM::RC) ok = ok && pre[i] >= 0;
-          const uint32_t off = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              i < NIK ? kr : vr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
-              16, off, 0, 0, 0);
+          off[i] = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
         }
       }
     } else {  // correction: pooled rows of the pruned blocks
@@ -445,14 +459,25 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
       for (int i = 0; i < NI; ++i) {
         const int row = fill_row(i, ln);
         const int c = fill_chunk(i, row, ln);
-        const int blk = cid[i % NIK];  // entry s.li + row, loaded a step earlier
+        const int blk = clampi(cid[i % NIK], 0, Nb - 1);  // entry s.li + row
         const bool ok = row < s.nkeys && c < GM::DG;
-        const uint32_t off = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            i < NIK ? pkr : pvr, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024),
-            16, off, 0, 0, 0);
+        off[i] = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
       }
-      load_cids(s.li + BN);  // the next correction step's entries
+    }
+    if (corr) load_cids(s.li + BN);  // the next correction step's entries
+    // (descriptors built from selected values: a select between two
+    // descriptors, or between two captured variables, is lowered through
+    // memory)
+    const rsrc_t rk = make_rsrc(pick(corr, pkh, kh), pick(corr, a.pooled_bytes, a.k_bytes));
+    const rsrc_t rv = make_rsrc(pick(corr, pvh, vh), pick(corr, a.pooled_bytes, a.v_bytes));
+    // (the builtin's arguments are plain locals: some argument expressions
+    // drop the kernel's host-side stub without a diagnostic)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const rsrc_t r = i < NIK ? rk : rv;
+      const uint32_t o = off[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024), 16, o, 0, 0, 0);
     }
   };
   // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
@@ -703,7 +728,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         mine[j * 64] = f32x4{s_new[0][4 * j], s_new[0][4 * j + 1], s_new[0][4 * j + 2], s_new[0][4 * j + 3]};
-      __syncthreads();
+      barrier_lds();
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4 v = theirs[j * 64];
