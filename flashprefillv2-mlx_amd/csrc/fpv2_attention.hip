@@ -337,8 +337,12 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // Exact steps are described 64 at a time: lane j of a window holds the
   // first key and valid-row count of step win_base + j, computed in one
   // vector pass from the selected list, and a step reads its pair with two
-  // readlanes.  Correction steps follow from the step index; each lane loads
-  // the pruned-list entries of its own fill rows one step ahead.
+  // readlanes.  With correction, the list entries of the next window are
+  // loaded one window ahead (win_next, raw; entries past the list row read
+  // as 0): a window computed from a load issued in the same step waits for
+  // every fill in flight (vmcnt(0)).  Without correction the kernel has no
+  // register for win_next (it would spill in the slice loop) and loads each
+  // window when it is reached.  Correction steps follow from the step index.
   int win_base = 0, win_key0 = 0, win_nk = 0;
   auto window_entry = [&](int it, int blk) {
     const int li = it / subs;
@@ -348,14 +352,14 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     win_key0 = key0;
     win_nk = (it >= n_sel || key0 > abs_last || n < 0) ? 0 : n;
   };
-  auto load_window = [&](int base) {
-    const int it = base + lane;
-    const int li = it / subs;  // < li_end when it < n_sel
-    window_entry(it, it < n_sel ? clampi(ids[li], 0, Nb - 1) : 0);
+  const rsrc_t idr = make_rsrc(ids, static_cast<uint32_t>(Nb) * 4u);
+  auto load_window = [&](int base) {  // raw entry of step base + lane
+    return static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(idr, ((base + lane) / subs) * 4, 0, 0));
   };
   // the first window's entries come from id_lane (its steps cover at most
   // the first 64 entries)
   window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
+  int win_next = CORR ? load_window(64) : 0;
   int walk_it = 0;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
@@ -363,7 +367,13 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     if (it < n_sel) {
       if (it - win_base >= 64) {
         win_base += 64;
-        load_window(win_base);
+        if constexpr (CORR) {
+          window_entry(win_base + lane, win_base + lane < n_sel ? clampi(win_next, 0, Nb - 1) : 0);
+          win_next = load_window(win_base + 64);
+        } else {
+          const int li = (win_base + lane) / subs;  // < li_end when the step is < n_sel
+          window_entry(win_base + lane, win_base + lane < n_sel ? clampi(ids[li], 0, Nb - 1) : 0);
+        }
       }
       s.key0 = __builtin_amdgcn_readlane(win_key0, it - win_base);
       s.nkeys = __builtin_amdgcn_readlane(win_nk, it - win_base);
@@ -943,6 +953,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     walk_it = 0;
     win_base = 0;
     window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
+    if constexpr (CORR) win_next = load_window(64);
     load_cids(0);
     run_walk(True{});
   }
