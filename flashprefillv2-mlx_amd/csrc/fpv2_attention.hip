@@ -680,7 +680,11 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
       bias[rg] = 0.f;
-      if constexpr (HP) bias[rg] = bias_of_ref(rg) + (p_pend.corr ? a.shift : 0.f);
+      // (the logit shift of correction slices selected as scalar bits, so
+      // the add takes it from an SGPR)
+      if constexpr (HP)
+        bias[rg] = bias_of_ref(rg) +
+                   __uint_as_float(__builtin_amdgcn_readfirstlane(p_pend.corr ? __float_as_uint(a.shift) : 0u));
     }
     u32x4 w[RG][2];
     // P for the pair of keys (2pi, 2pi+1) of the pending slice in row group
