@@ -150,21 +150,27 @@ def test_alpha_zero_equals_exact_causal_attention(cuda):
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
 
 
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+@pytest.mark.parametrize("mean_correction", [True, False])
 @pytest.mark.parametrize(("alpha", "min_steps"), [(0.0, 128), (0.02, 64)])
-def test_long_walk_crosses_step_windows(cuda, alpha, min_steps):
+def test_long_walk_crosses_step_windows(cuda, alpha, min_steps, mean_correction, head_dim):
     # up to 36 blocks of 128 keys = 144 exact 32-key steps for the last tiles:
     # the kernel describes exact steps 64 at a time, so the walk spans windows
-    config = FPV2Config(alpha=alpha, sink_tokens=128, window_tokens=384, mean_correction=True)
-    q, k, v = structured_qkv(length=4608, query_heads=4, kv_heads=1, head_dim=128, seed=59)
+    # (with correction the next window's entries are loaded a window ahead,
+    # without it when the window is reached)
+    config = FPV2Config(alpha=alpha, sink_tokens=128, window_tokens=384, mean_correction=mean_correction)
+    q, k, v = structured_qkv(length=4608, query_heads=4, kv_heads=1, head_dim=head_dim, seed=59)
     _, selected = _run_and_check(cuda, q, k, v, config)
     assert int(selected.cpu().sum(-1).max()) * 4 > min_steps
 
 
-def test_correction_phase_with_many_pruned_blocks(cuda):
-    # high-contrast clusters prune most blocks: the pooled phase spans > 64 entries
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+def test_correction_phase_with_many_pruned_blocks(cuda, head_dim):
+    # high-contrast clusters prune most blocks: the pooled phase spans > 64
+    # entries (several correction steps, each loading the next one's entries)
     config = FPV2Config(block_k=16, tile_q=16, alpha=0.5, sink_tokens=16, window_tokens=16,
                         mean_correction=True)
-    q, k, v = structured_qkv(length=2048, query_heads=4, kv_heads=2, head_dim=128,
+    q, k, v = structured_qkv(length=2048, query_heads=4, kv_heads=2, head_dim=head_dim,
                              block_size=16, noise=0.05, seed=53)
     _, selected = _run_and_check(cuda, q, k, v, config)
     pruned = (~selected.cpu()).sum(-1)
