@@ -25,8 +25,9 @@ same kernels run exact causal attention instead (``alpha = 0`` selects every
 visible block, and with no pruned block the correction is empty).
 
 With ``collect_stats`` the layer counts selected and visible blocks as the
-hook's ``block_sparsity`` does (``patch.py:66-88``): selected counts are summed
-on the device, and ``block_sparsity()`` synchronises once to read them.
+hook's ``block_sparsity`` does (``patch.py:66-88``): selected counts are kept
+on the device and summed in batches (``SelectedBlockCounter``), and
+``block_sparsity()`` synchronises once to read them.
 """
 
 from __future__ import annotations
@@ -37,8 +38,8 @@ import torch
 
 from fpv2 import _lib
 from fpv2.kernel import SUPPORTED_HEAD_DIMS
-from fpv2.patch import (_causal_block_count, _effective_config, _geometry, _pool_into,
-                        _request_config, _select_attend)
+from fpv2.patch import (SelectedBlockCounter, _causal_block_count, _effective_config, _geometry,
+                        _pool_into, _request_config, _select_attend)
 from fpv2.selection import FPV2Config
 
 
@@ -96,7 +97,7 @@ class ChunkedPrefill:
         self._complete = 0  # leading blocks pooled with all their rows
         self.pooled_rows = 0  # rows read by pooling so far (for accounting)
         self.collect_stats = collect_stats
-        self._selected = torch.zeros((), dtype=torch.int64, device=device)
+        self._selected = SelectedBlockCounter()
         self._visible = 0
 
     def reset(self) -> None:
@@ -106,7 +107,7 @@ class ChunkedPrefill:
         self.length = 0
         self._complete = 0
         self.pooled_rows = 0
-        self._selected.zero_()
+        self._selected.reset()
         self._visible = 0
 
     def block_sparsity(self) -> float:
@@ -114,7 +115,7 @@ class ChunkedPrefill:
         since construction or ``reset`` (0 when nothing was counted)."""
         if not self._visible:
             return 0.0
-        return 1.0 - int(self._selected.item()) / self._visible
+        return 1.0 - self._selected.value() / self._visible
 
     @staticmethod
     def _three_d(x: torch.Tensor, name: str) -> torch.Tensor:
@@ -220,7 +221,7 @@ class ChunkedPrefill:
                        self.pooled_v[:, :geo.num_blocks], geo, scale=call_scale, out=out,
                        marks=marks, keep=keep)
         if self.collect_stats:
-            self._selected += keep["lists"][1].sum(dtype=torch.int64)
+            self._selected.add(keep["lists"][1])
             self._visible += _causal_block_count(self.kv_heads, geo.query_length, geo.offset,
                                                  geo.config)
         return out[None]

@@ -41,10 +41,53 @@ except ImportError:  # pragma: no cover - older torch
 _ORIGINAL_SDPA = F.scaled_dot_product_attention
 _enabled = False
 _collect_stats = False
-# Selected blocks of FPV2 calls, summed on each call's device (0-d int64
-# tensors, one per device): accumulating costs one small kernel per call and
-# no host synchronisation; block_sparsity() reads them once.
-_selected_totals: dict[torch.device, torch.Tensor] = {}
+
+
+class SelectedBlockCounter:
+    """Sum of the selected-block counts of FPV2 calls on one device.
+
+    A call's ``counts`` tensor (a fresh ``[Hkv, Nt]`` int32 allocation) is
+    kept rather than reduced: every ``fold_every`` calls the kept tensors are
+    summed by one concatenation and one reduction into a 0-d int64 device
+    total, so a call launches no kernel and nothing synchronises until
+    ``value()`` is read.
+    """
+
+    def __init__(self, fold_every: int = 64) -> None:
+        self.fold_every = fold_every
+        self._pending: list[torch.Tensor] = []
+        self._total: torch.Tensor | None = None
+
+    def add(self, counts: torch.Tensor) -> None:
+        self._pending.append(counts)
+        if len(self._pending) >= self.fold_every:
+            self._fold()
+
+    def _fold(self) -> None:
+        if not self._pending:
+            return
+        part = torch.cat([c.reshape(-1) for c in self._pending]).sum(dtype=torch.int64)
+        self._total = part if self._total is None else self._total + part
+        self._pending.clear()
+
+    def device_total(self) -> torch.Tensor | None:
+        """The sum so far as a 0-d int64 device tensor (None if nothing was
+        added), without synchronising."""
+        self._fold()
+        return self._total
+
+    def value(self) -> int:
+        """The sum so far (synchronises once)."""
+        total = self.device_total()
+        return 0 if total is None else int(total.item())
+
+    def reset(self) -> None:
+        self._pending.clear()
+        self._total = None
+
+
+# Selected blocks of FPV2 calls, per device; block_sparsity() reads them once.
+_selected_totals: dict[torch.device, SelectedBlockCounter] = {}
 _selected_dense_blocks = 0
 _visible_blocks = 0
 _PACKED_TILE_ROWS = 128
@@ -92,7 +135,7 @@ def block_sparsity() -> float:
         return 0.0
     selected = _selected_dense_blocks
     for total in _selected_totals.values():
-        selected += int(total.item())
+        selected += total.value()
     return 1.0 - selected / _visible_blocks
 
 
@@ -226,9 +269,8 @@ def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out
         global _visible_blocks
         total = _selected_totals.get(counts.device)
         if total is None:
-            total = _selected_totals[counts.device] = torch.zeros(
-                (), dtype=torch.int64, device=counts.device)
-        total += counts.sum(dtype=torch.int64)
+            total = _selected_totals[counts.device] = SelectedBlockCounter()
+        total.add(counts)
         _visible_blocks += _causal_block_count(kv_heads, geo.query_length, geo.offset, config)
     if out is None:
         out = torch.empty((geo.query_heads, geo.query_length, geo.head_dim),

@@ -271,7 +271,8 @@ class ChunkedPrefillRunner:
         visible = sum(c._visible for c in self.caches)
         if not visible:
             return 0.0
-        selected = int(sum(c._selected for c in self.caches).item())
+        totals = [t for t in (c._selected.device_total() for c in self.caches) if t is not None]
+        selected = int(torch.stack(totals).sum().item()) if totals else 0  # one synchronisation
         return 1.0 - selected / visible
 
     def _layer(self, li: int, x: torch.Tensor, delta: torch.Tensor | None, cos, sin):

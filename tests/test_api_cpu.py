@@ -367,3 +367,21 @@ def test_chunked_request_config_follows_the_hook_gates():
     assert cp.request_config(2048).alpha == 0.0
     cp.length = 6000
     assert cp.request_config(2048).last_n_blocks == 0
+
+
+def test_selected_block_counter_folds_in_batches():
+    """Selected counts are kept and summed in batches; the total is exact
+    across batches, partial batches and a reset."""
+    from fpv2.patch import SelectedBlockCounter
+    counter = SelectedBlockCounter(fold_every=4)
+    g = torch.Generator().manual_seed(3)
+    tensors = [torch.randint(0, 1000, (2, 1 + i % 5), generator=g, dtype=torch.int32) for i in range(11)]
+    for t in tensors:
+        counter.add(t)
+    assert len(counter._pending) == 11 % 4  # two folds happened
+    assert counter.value() == sum(int(t.sum()) for t in tensors)
+    assert not counter._pending
+    counter.add(torch.full((3,), 2**30, dtype=torch.int32))  # int64 accumulation
+    assert counter.value() == sum(int(t.sum()) for t in tensors) + 3 * 2**30
+    counter.reset()
+    assert counter.value() == 0
