@@ -119,33 +119,6 @@ def check_text(text: str, symbol_filter: str = "sparse_attn_kernel") -> list[str
     return errors
 
 
-def check_no_static_lds(text: str, symbol_filter: str) -> list[str]:
-    """Kernels matching `symbol_filter` must declare no static LDS (their
-    metadata's .group_segment_fixed_size is 0), so that the dynamic LDS area
-    starts at address 0."""
-    errors: list[str] = []
-    entries: list[dict] = []
-    in_kernels = False
-    for line in text.splitlines():
-        if line.startswith("amdhsa.kernels:"):
-            in_kernels = True
-            continue
-        if not in_kernels:
-            continue
-        if line.startswith("  - ."):  # a new kernel entry (its first key on this line)
-            entries.append({})
-            line = "    " + line[4:]
-        if entries and line.startswith("    .") and not line.startswith("     "):
-            key, _, value = line.strip().partition(":")
-            entries[-1][key] = value.strip()
-    for e in entries:
-        name = e.get(".name", "")
-        if symbol_filter in name and int(e.get(".group_segment_fixed_size", "0")) != 0:
-            errors.append(f"{name}: static LDS of {e['.group_segment_fixed_size']} bytes "
-                          "in front of the dynamic area")
-    return errors
-
-
 def main(argv: list[str]) -> int:
     text = open(argv[1]).read()
     errors = check_text(text, argv[2] if len(argv) > 2 else "sparse_attn_kernel")

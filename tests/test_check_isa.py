@@ -89,17 +89,3 @@ def test_lds_write_may_stay_in_flight_across_back_edge():
     counted = _fn("\tds_read_b128 v[80:83], v84\n\tds_write_b32 v3, v4\n\ts_waitcnt lgkmcnt(1)\n"
                   "\tv_mov_b32_e32 v1, v81\n")
     assert check_isa.check_text(counted) == []
-
-
-def test_static_lds_check_reads_kernel_metadata():
-    meta = ("amdhsa.kernels:\n"
-            "  - .agpr_count:     0\n"
-            "    .args:\n"
-            "      - .offset:         0\n"
-            "    .group_segment_fixed_size: 0\n"
-            "    .name:           k_select_ring_kernel_a\n"
-            "  - .agpr_count:     0\n"
-            "    .group_segment_fixed_size: 560\n"
-            "    .name:           k_select_ring_kernel_b\n")
-    errors = check_isa.check_no_static_lds(meta, "select_ring_kernel")
-    assert len(errors) == 1 and "k_select_ring_kernel_b" in errors[0] and "560" in errors[0]
