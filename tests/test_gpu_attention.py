@@ -240,3 +240,45 @@ def test_outlier_with_correction_phase(cuda):
     q, k, v = _planted_outlier(2048, strength=40.0, seed=22)
     config = FPV2Config(alpha=0.5, sink_tokens=128, window_tokens=128, tile_q=32)
     _run_and_check(cuda, q, k, v, config)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_crafted_lists_at_window_and_correction_boundaries(cuda, head_dim):
+    # 32-key blocks, so one selected block is one exact step: tiles whose
+    # selected blocks [0, s) + the diagonal give 63..130 exact steps (the
+    # 64-step list windows, loaded a window ahead) and whose pruned blocks
+    # [s, t) give 31..65 pooled entries (correction steps of 32 entries,
+    # each loading the next step's list entries), compared with the oracle
+    # on the same selection and pooled values
+    config = FPV2Config(block_k=32, tile_q=32, alpha=0.1, mean_correction=True)
+    length, hq, hkv = 8192, 4, 1
+    nt = nb = length // 32
+    g = torch.Generator().manual_seed(71)
+    q, k, v = structured_qkv(length=length, query_heads=hq, kv_heads=hkv, head_dim=head_dim,
+                             block_size=32, seed=71)
+    selected = torch.rand((hkv, nt, nb), generator=g) < 0.3
+    selected &= torch.arange(nb)[None, None, :] <= torch.arange(nt)[None, :, None]  # causal
+    crafted = {}
+    for s in (62, 63, 64, 127, 128):
+        for p in (31, 32, 33, 64, 65):
+            crafted.setdefault(s + p, s)
+    for t, s in crafted.items():
+        selected[:, t] = False
+        selected[:, t, :s] = True
+    selected[:, torch.arange(nt), torch.arange(nt)] = True  # the diagonal block
+    dtype = torch.bfloat16
+    qd, kd, vd = (x.to(dtype).to(cuda) for x in (q, k, v))
+    pk = pool_blocks(kd, config.block_k)
+    pv = pool_blocks(vd, config.block_k)
+    sel_dev = selected.to(cuda)
+    lists = compact_block_indices(sel_dev, config=config, query_length=length, key_length=length)
+    counts, pcounts = lists[1].cpu(), lists[3].cpu()
+    for t, s in crafted.items():
+        assert int(counts[0, t]) == s + 1 and int(pcounts[0, t]) == t - s
+    out = sparse_attention(qd, kd, vd, pk, pv, *lists, scale=head_dim ** -0.5, config=config)
+    torch.cuda.synchronize()
+    qn, kn, vn = (to_np(x.to(dtype)) for x in (q, k, v))
+    ref = orc.fpv2_attention_blockwise(qn, kn, vn, scale=head_dim ** -0.5, selected=selected.numpy(),
+                                       pooled_k=to_np(pk), pooled_v=to_np(pv), config=_cfg(config))
+    err = attention_errors(to_np(out), ref)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
