@@ -189,9 +189,13 @@ struct Step {
 };
 
 // DS = 2: two waves share each 32-row group, each owning half of the head
-// dimension: each multiplies its half of Q and K into a partial S, the two
-// partials are summed through LDS, both compute P, and each accumulates its
-// half of O.  This keeps D = 256 at two waves per SIMD within 256 registers.
+// dimension: each multiplies its half of Q and K into a partial S.  Each
+// wave of the pair also owns half of the slice's 32 keys: it sums the two
+// partials of its 16 keys, computes their P and row sum, and hands its P to
+// the partner through LDS at the same barrier as the partial S, so the
+// softmax work is not repeated.  Each accumulates its half of O from both
+// halves of P.  This keeps D = 256 at two waves per SIMD within 256
+// registers.
 // RG = 2: a wave owns two 32-row groups that share every K/V fragment read
 // from LDS; with the whole 512-entry register file of its SIMD (one wave per
 // SIMD) the two groups' matrix and softmax work interleave within the wave.
@@ -205,6 +209,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   constexpr bool kAsm = D <= 128 || DS == 2;
   constexpr int DT = GM::DT / DS;  // 32-wide output column tiles of this wave
   constexpr int KSQ = GM::KS / DS; // 16-deep QK k-steps of this wave
+  // DS = 2: S element j < 8 of a wave holds one of its own 16 keys (keys
+  // 0-15 for the first wave of the pair, 16-31 for the second, which reads
+  // its K rows rotated by 16); elements 8-15 hold the partner's keys.
+  constexpr bool KSPLIT = DS == 2;
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = GM::BN;
   constexpr int ROWB = GM::ROWB;
@@ -213,8 +221,9 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   constexpr int NI = 2 * NIK;             // ... per stage (K then V)
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
   static_assert(NST >= 2 && NI * (NST - 2) <= 63, "vmcnt range");
-  // the stage ring, then (DS = 2) each wave's partial S (64 lanes x 16
-  // floats) for its partner
+  // the stage ring, then (DS = 2) 4 KiB per wave for its partner: bytes
+  // [0, 1024) its P (16 bytes per lane), [1024, 1280) a float per lane (row
+  // max, row sum), [2048, 4096) its partial S of the partner's keys
   __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE + (DS == 2 ? WAVES * 4096 : 0)];
   uint8_t* const xbuf = smem + NST * GM::STAGE;
 
@@ -544,11 +553,14 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // 16u + 4hf + (lane&15)/4 (+8), dims 32dt + ... -> (vbase ^ 64dt) +
   // (16u (+8)) * ROWB.  The XOR terms only touch bits below 9, and slice
   // offsets are multiples of 32 rows, so slice offsets add outside the XOR.
-  const int km = GM::kmask(l32);
+  // (DS = 2: the second wave of a pair reads key row l32 ^ 16, which has the
+  // same swizzle, so its S elements 0-7 hold keys 16-31)
+  const int krow = KSPLIT ? (l32 ^ (16 * dhalf)) : l32;
+  const int km = GM::kmask(krow);
   // (DS = 2: this wave's k-steps start 32*KSQ bytes along the row, above
   // the swizzled bits)
   const uint32_t kbase =
-      (smem_lds + l32 * ROWB + ((16 * hf) ^ (16 * km))) ^ static_cast<uint32_t>(dhalf * KSQ * 32);
+      (smem_lds + krow * ROWB + ((16 * hf) ^ (16 * km))) ^ static_cast<uint32_t>(dhalf * KSQ * 32);
   const int tr_row = (lane & 15) >> 2;
   const int cig = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // chunk within a 64-byte group
   const int vq = ROWB >= 256 ? tr_row : ((tr_row >> 1) & 1);   // swizzled 64-byte group
@@ -557,6 +569,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   const uint32_t vbase =
       (smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8) ^
       static_cast<uint32_t>(dhalf * DT * 64);
+  // DS = 2: V^T rows of the wave's own 16 keys (first P operand) and of the
+  // partner's (second), 16 rows apart; the swizzle repeats every 4 rows.
+  const uint32_t vbase_own = vbase + (KSPLIT ? dhalf * 16 * ROWB : 0);
+  const uint32_t vbase_oth = vbase + (KSPLIT ? (1 - dhalf) * 16 * ROWB : 0);
 
   // ---- slice pipeline ----
   // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
@@ -611,16 +627,19 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   constexpr int kMaxDelay = FPV2_MAX_DELAY; // PV MFMAs issued before the first row-max step
   constexpr int PER_BATCH = 4;        // MFMA operands per batch of 8 transposing reads
   constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
-  auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8]) {
+  // (va: V^T rows of the first P operand's keys, va2: of the second's; with
+  // DS = 1 the second operand's rows follow at 16 rows from va)
+  auto issue_v = [&](uint32_t va, uint32_t va2, auto bc, u32x2 (&r)[8]) {
     constexpr int b = decltype(bc)::value;
     StaticFor<0, PER_BATCH>::run([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int op = b * PER_BATCH + q;
       if constexpr (op < PV_OPS) {
         constexpr int u = op / DT, dt = op % DT;
-        const uint32_t addr = va ^ (64 * dt);
-        r[2 * q] = lds_read_tr<kAsm, u * 16 * ROWB>(addr);
-        r[2 * q + 1] = lds_read_tr<kAsm, (u * 16 + 8) * ROWB>(addr);
+        constexpr int R0 = KSPLIT ? 0 : u * 16 * ROWB;
+        const uint32_t addr = ((KSPLIT && u == 1) ? va2 : va) ^ (64 * dt);
+        r[2 * q] = lds_read_tr<kAsm, R0>(addr);
+        r[2 * q + 1] = lds_read_tr<kAsm, R0 + 8 * ROWB>(addr);
       } else {
         r[2 * q] = u32x2{0u, 0u};
         r[2 * q + 1] = u32x2{0u, 0u};
@@ -647,7 +666,8 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     f32x16(&s_new)[RG] = s_buf[B];
     f32x16(&s_old)[RG] = s_buf[1 - B];
     constexpr int KW = KSQ < 4 ? KSQ : 4;  // K fragment reads in flight
-    const uint32_t va = vbase + p_pend.off;
+    const uint32_t va = vbase_own + p_pend.off;
+    const uint32_t va2 = vbase_oth + p_pend.off;
     const uint32_t ka = kbase + nw.off;
     u32x2 vb[2][8];
     u32x4 kf[KSQ];
@@ -674,7 +694,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
       for (int rg = 0; rg < RG; ++rg) s_new[rg] = f32x16{};
     }
     // V^T batch 0 after the first K window: those K reads do not wait behind it
-    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
+    if constexpr (HP) issue_v(va, va2, std::integral_constant<int, 0>{}, vb[0]);
     constexpr int NV0 = HP ? 2 * PER_BATCH : 0;  // reads of batch 0
     float bias[RG];
 #pragma unroll
@@ -699,12 +719,13 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
       w[rg][pi / 4][pi % 4] = word;
       asm volatile("" ::"v"(word));
     };
-    constexpr int NP = 8 * RG;  // exp pairs per slice
+    // exp pairs per slice (DS = 2: the wave's own 16 keys, S elements 0-7)
+    constexpr int NP = KSPLIT ? 4 : 8 * RG;
     if constexpr (HN) {
       // kExpLead pairs first, while the first K fragments are in flight,
       // then the rest spread over the QK MFMAs.
       constexpr int E0 = HP ? kExpLead * RG : 0;
-      constexpr int EA = kExpA * RG;
+      constexpr int EA = KSPLIT ? NP : kExpA * RG;  // (DS = 2: all before the exchange)
       if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
       StaticFor<0, KSQ>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
@@ -724,31 +745,41 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     } else if constexpr (HP) {
       StaticFor<0, NP>::run(exp_pair);
     }
-    constexpr int EB = HN ? kExpA * RG : NP;  // pairs done once stage A ends
+    constexpr int EB = (HN && !KSPLIT) ? kExpA * RG : NP;  // pairs done once stage A ends
     if constexpr (HP) {
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
         pb[rg][0] = as_vec8<T>(w[rg][0]);
-        if constexpr (EB == NP) pb[rg][1] = as_vec8<T>(w[rg][1]);
+        if constexpr (EB == NP && !KSPLIT) pb[rg][1] = as_vec8<T>(w[rg][1]);
       }
     }
 
-    // DS = 2: add the partner's partial S (every wave of the workgroup takes
+    // DS = 2: exchange with the partner wave: the partial S of its keys
+    // (elements 8-15) for the partner's partial of ours, added to elements
+    // 0-7, and the P of the pending slice's own keys for the partner's P,
+    // the second P operand of stage B.  Every wave of the workgroup takes
     // this path in the same calls, so the barrier is uniform; the next write
-    // follows the next sub-tile's barrier, after the partner's read)
-    if constexpr (HN && DS == 2) {
-      f32x4* mine = reinterpret_cast<f32x4*>(xbuf + wave * 4096) + lane;
-      const f32x4* theirs = reinterpret_cast<const f32x4*>(xbuf + (wave ^ (WAVES / 2)) * 4096) + lane;
+    // follows the next sub-tile's barrier, after the partner's reads.
+    if constexpr ((HN || HP) && KSPLIT) {
+      uint8_t* const mine = xbuf + wave * 4096;
+      const uint8_t* const theirs = xbuf + (wave ^ (WAVES / 2)) * 4096;
+      if constexpr (HN) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        mine[j * 64] = f32x4{s_new[0][4 * j], s_new[0][4 * j + 1], s_new[0][4 * j + 2], s_new[0][4 * j + 3]};
-      barrier_lds();
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x4 v = theirs[j * 64];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s_new[0][4 * j + e] += v[e];
+        for (int j = 0; j < 2; ++j)
+          reinterpret_cast<f32x4*>(mine + 2048)[j * 64 + lane] =
+              f32x4{s_new[0][8 + 4 * j], s_new[0][9 + 4 * j], s_new[0][10 + 4 * j], s_new[0][11 + 4 * j]};
       }
+      if constexpr (HP) reinterpret_cast<u32x4*>(mine)[lane] = w[0][0];
+      barrier_lds();
+      if constexpr (HN) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const f32x4 v = reinterpret_cast<const f32x4*>(theirs + 2048)[j * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s_new[0][4 * j + e] += v[e];
+        }
+      }
+      if constexpr (HP) pb[0][1] = as_vec8<T>(reinterpret_cast<const u32x4*>(theirs)[lane]);
     }
 
     // mask of the new slice (diagonal / partial slices only)
@@ -757,12 +788,14 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
       // it is kept iff e < nkeys and (correction, or e <= qpos - key0), i.e.
       // iff c_j <= lim with one per-lane limit, so the 16 tests compare
       // against immediates.
+      // (DS = 2: only elements 0-7, whose keys are 16 higher for the
+      // second wave of a pair)
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
-        int lim = nw.nkeys - 1 - hf * 4;
-        if (!nw.corr) lim = min(lim, qpos_abs[rg] - nw.key0 - hf * 4);
+        int lim = nw.nkeys - 1 - hf * 4 - (KSPLIT ? 16 * dhalf : 0);
+        if (!nw.corr) lim = min(lim, qpos_abs[rg] - nw.key0 - hf * 4 - (KSPLIT ? 16 * dhalf : 0));
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < (KSPLIT ? 8 : 16); ++j) {
           const int cj = (j >> 2) * 8 + (j & 3);
           s_new[rg][j] = cj <= lim ? s_new[rg][j] : neg_inf();
         }
@@ -787,7 +820,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
       lgkm_wait<kAsm, 0>(vb[0]);
       StaticFor<0, BATCHES>::run([&](auto bc) {
         constexpr int b = decltype(bc)::value;
-        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
+        if constexpr (b + 1 < BATCHES) issue_v(va, va2, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
         StaticFor<0, PER_BATCH>::run([&](auto qc) {
           constexpr int q = decltype(qc)::value;
           constexpr int op = b * PER_BATCH + q;
@@ -820,11 +853,23 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     }
 
     // ---- stage C: reference max of the new slice ----
+    // (DS = 2: the max over the wave's own keys, then over the partner's
+    // through LDS; the partner's previous read of this word was consumed
+    // before the barrier of this sub-tile)
+    auto row_max = [&](int rg) {
+      float m = pair_max(mx[rg]);
+      if constexpr (KSPLIT) {
+        reinterpret_cast<float*>(xbuf + wave * 4096 + 1024)[lane] = m;
+        barrier_lds();
+        m = fmaxf(m, reinterpret_cast<const float*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane]);
+      }
+      return m;
+    };
     if constexpr (MAX && MODE == 1) {
       // the first slice: O and l are still zero, no rescale
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
-        m_ref[rg] = fmaf(pair_max(mx[rg]), c_pos, nw.corr ? a.shift : 0.f);
+        m_ref[rg] = fmaf(row_max(rg), c_pos, nw.corr ? a.shift : 0.f);
         neg_m[rg] = (m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg];
         m_thr[rg] = m_ref[rg] + kRescaleSlack;
       }
@@ -832,7 +877,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     if constexpr (MAX && MODE == 2) {
 #pragma unroll
       for (int rg = 0; rg < RG; ++rg) {
-        const float m_cand = fmaf(pair_max(mx[rg]), c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
+        const float m_cand = fmaf(row_max(rg), c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
         if (__ballot(m_cand > thr_of_ref(rg)) != 0ull) {
           const float m_new = fmaxf(m_ref[rg], m_cand);
           const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
@@ -924,11 +969,24 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // bfloat16 P hold it unless the range is exceeded.  A valid row whose sum
   // leaves [2^-60, 2^100] (or is NaN) sends the workgroup through the walk
   // again with the online reference and rescale (kernel.py:287-310).
+  // DS = 2: row sums over all keys, the two waves' sums of their own keys
+  // added in either order, so both waves hold the same value.
+  float l_pair = 0.f;
+  auto pair_row_sum = [&]() {
+    if constexpr (KSPLIT) {
+      l_pair = pair_sum(l_run[0]);
+      reinterpret_cast<float*>(xbuf + wave * 4096 + 1024)[lane] = l_pair;
+      barrier_lds();
+      l_pair += reinterpret_cast<const float*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane];
+    }
+  };
+  auto row_sum = [&](int rg) { return KSPLIT ? l_pair : pair_sum(l_run[rg]); };
   run_walk(False{});
+  pair_row_sum();
   bool bad = false;
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
-    const float l = pair_sum(l_run[rg]);
+    const float l = row_sum(rg);
     bad = bad || (row_valid[rg] && !(l >= 0x1p-60f && l <= 0x1p100f));
   }
   // Workgroup-wide decision through the last ring stage, which the second
@@ -960,13 +1018,14 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     if constexpr (CORR) win_next = load_window(64);
     load_cids(0);
     run_walk(True{});
+    pair_row_sum();
   }
 
   // ---- normalise and store ----
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
     if constexpr (kAccA) agpr_fence(o[rg]);
-    const float l_tot = pair_sum(l_run[rg]);
+    const float l_tot = row_sum(rg);
     if (!exists[rg] || pos[rg] >= a.out_rows) continue;
     const float inv = (row_valid[rg] && l_tot > 0.f) ? 1.f / l_tot : 0.f;
     uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g[rg]) * a.o_hs + pos[rg] * a.o_rs;

@@ -134,9 +134,10 @@ def test_gqa_ratios_and_tile_rows(cuda, group, tile_q):
     _run_and_check(cuda, q, k, v, config)
 
 
-def test_float16_path(cuda):
+@pytest.mark.parametrize("head_dim", [64, 96, 128, 256])
+def test_float16_path(cuda, head_dim):
     config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256)
-    q, k, v = structured_qkv(length=1024, query_heads=8, kv_heads=2, head_dim=128, seed=47)
+    q, k, v = structured_qkv(length=1024, query_heads=8, kv_heads=2, head_dim=head_dim, seed=47)
     _run_and_check(cuda, q, k, v, config, dtype=torch.float16)
 
 
@@ -218,26 +219,32 @@ def _planted_outlier(length, *, strength, seed, hq=8, hkv=2, d=128):
     # no second walk
     (24.0, "large"),
 ])
-def test_logits_far_above_the_first_slice(cuda, strength, what):
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_logits_far_above_the_first_slice(cuda, strength, what, head_dim):
     """Rows whose largest logit comes late in the walk and far above every
     key of the first slice: attention still matches the oracle.  The fixed
     first-slice reference either holds the range or sends the workgroup
     through the online-reference walk (kernel.py:287-310 rescales per key
-    block instead)."""
-    q, k, v = _planted_outlier(1024, strength=strength, seed=21)
+    block instead).  head_dim 256 splits each row's keys between two waves,
+    which combine their row maxima and sums through LDS."""
+    # the same logit gap at every head dimension (strength**2 / sqrt(d))
+    s = strength * (head_dim / 128) ** 0.25
+    q, k, v = _planted_outlier(1024, strength=s, seed=21, d=head_dim)
     config = FPV2Config(alpha=0.0, sink_tokens=0, window_tokens=0, last_n_blocks=0,
                         mean_correction=False, tile_q=32)
     got, _ = _run_and_check(cuda, q, k, v, config)
     exact = orc.exact_causal_attention(to_np(q.bfloat16()), to_np(k.bfloat16()),
-                                       to_np(v.bfloat16()), 128 ** -0.5)
+                                       to_np(v.bfloat16()), head_dim ** -0.5)
     err = attention_errors(got, exact)
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
 
 
-def test_outlier_with_correction_phase(cuda):
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_outlier_with_correction_phase(cuda, head_dim):
     """The same late outlier with pruning and mean correction on (alpha 0.5):
     the second walk repeats the exact and the correction phases."""
-    q, k, v = _planted_outlier(2048, strength=40.0, seed=22)
+    s = 40.0 * (head_dim / 128) ** 0.25
+    q, k, v = _planted_outlier(2048, strength=s, seed=22, d=head_dim)
     config = FPV2Config(alpha=0.5, sink_tokens=128, window_tokens=128, tile_q=32)
     _run_and_check(cuda, q, k, v, config)
 
@@ -282,3 +289,31 @@ def test_crafted_lists_at_window_and_correction_boundaries(cuda, head_dim):
                                        pooled_k=to_np(pk), pooled_v=to_np(pv), config=_cfg(config))
     err = attention_errors(to_np(out), ref)
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_head_dim_256_reruns_are_bitwise_identical(cuda, dtype):
+    """head_dim 256 exchanges partial logits, P and row statistics between
+    the two waves of each row group through LDS: repeated launches on the
+    same lists give bit-identical outputs, and both halves of every row's
+    head dimension are normalised by the same row sum (the output matches
+    the oracle on each half)."""
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256, mean_correction=True)
+    q, k, v = structured_qkv(length=2048, query_heads=8, kv_heads=2, head_dim=256, seed=53,
+                             dtype=dtype, device=cuda)
+    scale = 256 ** -0.5
+    pk, pv = pool_blocks(k, config.block_k), pool_blocks(v, config.block_k)
+    selected, _ = block_scores_and_select(q, pk, scale=scale, config=config)
+    lists = compact_block_indices(selected, config=config, query_length=q.shape[1],
+                                  key_length=k.shape[1])
+    outs = [sparse_attention(q, k, v, pk, pv, *lists, scale=scale, config=config) for _ in range(3)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    same = orc.fpv2_attention_blockwise(to_np(q), to_np(k), to_np(v), scale=scale,
+                                        selected=to_np(selected), pooled_k=to_np(pk),
+                                        pooled_v=to_np(pv), config=_cfg(config))
+    got = to_np(outs[0])
+    for half in (slice(0, 128), slice(128, 256)):
+        err = attention_errors(got[..., half], same[..., half])
+        assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
