@@ -1,0 +1,121 @@
+"""GPU parity over seeded random combinations of the operator's parameters.
+
+Each case draws head_dim, dtype, query/KV head counts, block_k, tile_q,
+alpha, sink/window/tail settings, mean correction, a chunk offset, an
+unaligned query length and the sign of the scale, then runs the public
+operators in sequence (``pool_blocks`` -> ``block_scores_and_select`` ->
+``compact_block_indices`` -> ``sparse_attention``, the hook's data flow in
+``fpv2/patch.py:109-174``) and checks every stage against the oracle:
+
+  * pooled K/V bit-exact (``selection.py:68-80``);
+  * block decisions equal outside the 1e-4 band around alpha
+    (``selection.py:174-195``);
+  * block lists and counts equal to the oracle's compaction of the device
+    mask, bit for bit (``kernel.py:141-184``);
+  * outputs of the valid query rows against the oracle's blockwise float32
+    evaluation with the device's selection and pooled values
+    (``reference.py:55-90``): max-abs <= 2e-2, mean-abs <= 2e-3.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import attention_errors, to_np
+from oracle import fpv2_oracle as orc
+from fpv2 import FPV2Config, pool_blocks
+from fpv2.kernel import compact_block_indices, sparse_attention
+from fpv2.selection import block_scores_and_select
+from fpv2.synthetic import structured_qkv
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS, BAND = 2e-2, 2e-3, 1e-4
+_DT = {torch.bfloat16: "bf16", torch.float16: "f16"}
+
+
+def _draw_cases(n: int, seed: int = 20261202) -> list[dict]:
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        d = int(rng.choice([64, 96, 128, 256]))
+        bk = int(rng.choice([16, 32, 64, 128]))
+        hkv = int(rng.choice([1, 2]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        cases.append(dict(
+            case=i, head_dim=d, dtype=[torch.bfloat16, torch.float16][int(rng.integers(2))],
+            kv_heads=hkv, query_heads=hkv * g, block_k=bk, tile_q=int(rng.choice([16, 32, 64])),
+            alpha=float(rng.choice([0.0, 0.05, 0.15, 0.5])),
+            sink=int(rng.choice([0, 1, 2])) * bk, window=int(rng.choice([0, 1, 3])) * bk,
+            last_n=int(rng.integers(0, 3)), corr=bool(rng.integers(2)),
+            offset=int(rng.choice([0, int(rng.integers(1, 600))])),
+            qlen=int(rng.integers(100, 700)), sign=float(rng.choice([1.0, 1.0, 1.0, -1.0])),
+            seed=int(rng.integers(1 << 30))))
+    return cases
+
+
+CASES = _draw_cases(48)
+
+
+def _id(c: dict) -> str:
+    return (f"c{c['case']}-d{c['head_dim']}-{_DT[c['dtype']]}-g{c['query_heads'] // c['kv_heads']}"
+            f"-bk{c['block_k']}-tq{c['tile_q']}-a{c['alpha']}-corr{int(c['corr'])}"
+            f"-off{c['offset']}-L{c['qlen']}{'-neg' if c['sign'] < 0 else ''}")
+
+
+@pytest.mark.parametrize("c", CASES, ids=[_id(c) for c in CASES])
+def test_random_configuration_matches_oracle(cuda, c):
+    d, dtype, bk, tq = c["head_dim"], c["dtype"], c["block_k"], c["tile_q"]
+    hq, hkv, offset, qlen = c["query_heads"], c["kv_heads"], c["offset"], c["qlen"]
+    config = FPV2Config(block_k=bk, tile_q=tq, alpha=c["alpha"], sink_tokens=c["sink"],
+                        window_tokens=c["window"], last_n_blocks=c["last_n"],
+                        mean_correction=c["corr"])
+    ocfg = orc.OracleConfig(**{f: getattr(config, f) for f in orc.OracleConfig.__dataclass_fields__})
+    scale = c["sign"] * d ** -0.5
+    lk = offset + qlen  # the queries are the last qlen keys (lower-right causal)
+    q, k, v = structured_qkv(length=lk, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bk,
+                             seed=c["seed"], dtype=dtype)
+    # tile-padded queries and block-padded keys, zero past the valid lengths
+    lq_pad = -(-qlen // tq) * tq
+    nb = -(-(offset + lq_pad) // bk)
+    qp = torch.zeros((hq, lq_pad, d), dtype=dtype)
+    qp[:, :qlen] = q[:, offset:]
+    kp = torch.zeros((hkv, nb * bk, d), dtype=dtype)
+    vp = torch.zeros((hkv, nb * bk, d), dtype=dtype)
+    kp[:, :lk] = k
+    vp[:, :lk] = v
+    qd, kd, vd = qp.to(cuda), kp.to(cuda), vp.to(cuda)
+
+    pk, pv = pool_blocks(kd, bk), pool_blocks(vd, bk)
+    qn, kn, vn = to_np(qp), to_np(kp), to_np(vp)
+    assert np.array_equal(to_np(pk), orc.pool_blocks(kn, bk, out_dtype=_DT[dtype]))
+    assert np.array_equal(to_np(pv), orc.pool_blocks(vn, bk, out_dtype=_DT[dtype]))
+
+    sel, _ = block_scores_and_select(qd, pk, scale=scale, config=config, offset=offset,
+                                     query_length=qlen)
+    sel_o, _, ratio = orc.block_scores_and_select(qn, to_np(pk), scale=scale, config=ocfg,
+                                                  offset=offset, query_length=qlen,
+                                                  return_ratio=True)
+    sel_d = to_np(sel)
+    differ = (sel_d != sel_o) & ~(np.abs(ratio - config.alpha) <= BAND)
+    assert not differ.any(), f"{int(differ.sum())} block decisions differ outside the band"
+
+    lists = compact_block_indices(sel, config=config, offset=offset, query_length=qlen,
+                                  key_length=lk)
+    want_lists = orc.compact_block_indices(sel_d, config=ocfg, offset=offset,
+                                           query_length=qlen, key_length=lk)
+    for got_l, want_l in zip(lists, want_lists):
+        assert np.array_equal(to_np(got_l), want_l)
+
+    out = sparse_attention(qd, kd, vd, pk, pv, *lists, scale=scale, config=config,
+                           offset=offset, query_length=qlen, key_length=lk)
+    torch.cuda.synchronize()
+    want = orc.fpv2_attention_blockwise(qn, kn, vn, scale=scale, selected=sel_d,
+                                        pooled_k=to_np(pk), pooled_v=to_np(pv), config=ocfg,
+                                        offset=offset, query_length=qlen, key_length=lk)
+    got = to_np(out)[:, :qlen]
+    assert np.isfinite(got).all()
+    err = attention_errors(got, want[:, :qlen])
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
