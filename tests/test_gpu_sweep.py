@@ -119,3 +119,93 @@ def test_random_configuration_matches_oracle(cuda, c):
     assert np.isfinite(got).all()
     err = attention_errors(got, want[:, :qlen])
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
+# ---------------------------------------------------------------------------
+# The SDPA hook (fpv2/patch.py:177-285 restated in fpv2/patch.py): random
+# eligible calls through torch.nn.functional.scaled_dot_product_attention.
+# ---------------------------------------------------------------------------
+
+def _draw_hook_cases(n: int, seed: int = 1202) -> list[dict]:
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        d = int(rng.choice([64, 96, 128, 256]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        hkv = int(rng.choice([1, 2])) if d * g * 2 > 1024 else int(rng.choice([1, 2, 4]))
+        hkv = max(1, min(hkv, 2048 // (d * g)))  # bounded oracle work
+        tile_q = int(rng.choice([128, 128, 64, 32]))
+        lk = int(rng.integers(200, 1400))
+        lq = lk if rng.random() < 0.5 else int(rng.integers(128, lk + 1))
+        cases.append(dict(
+            case=i, head_dim=d, dtype=[torch.bfloat16, torch.float16][int(rng.integers(2))],
+            kv_heads=hkv, query_heads=hkv * g, tile_q=tile_q,
+            block_k=int(rng.choice([32, 64, 128])), alpha=float(rng.choice([0.05, 0.1, 0.3])),
+            sink=int(rng.choice([0, 128])), window=int(rng.choice([0, 128, 384])),
+            last_n=int(rng.choice([0, 2])), corr=bool(rng.integers(2)), lk=lk, lq=lq,
+            total=bool(rng.integers(2)), scale=float(rng.choice([1.0, 0.7])) * d ** -0.5,
+            seed=int(rng.integers(1 << 30))))
+    return cases
+
+
+HOOK_CASES = _draw_hook_cases(24)
+
+
+def _hook_id(c: dict) -> str:
+    return (f"h{c['case']}-d{c['head_dim']}-{_DT[c['dtype']]}-g{c['query_heads'] // c['kv_heads']}"
+            f"-tq{c['tile_q']}-bk{c['block_k']}-a{c['alpha']}-corr{int(c['corr'])}"
+            f"-Lq{c['lq']}-Lk{c['lk']}{'-tail' if c['total'] else ''}")
+
+
+@pytest.mark.parametrize("c", HOOK_CASES, ids=[_hook_id(c) for c in HOOK_CASES])
+def test_random_hook_call_matches_oracle(cuda, c):
+    import torch.nn.functional as F
+    from torch.nn.attention.bias import causal_lower_right
+    import fpv2.patch as patch
+    from fpv2 import block_sparsity, disable, enable
+
+    d, dtype, lq, lk = c["head_dim"], c["dtype"], c["lq"], c["lk"]
+    hq, hkv = c["query_heads"], c["kv_heads"]
+    config = FPV2Config(block_k=c["block_k"], tile_q=c["tile_q"], alpha=c["alpha"],
+                        sink_tokens=c["sink"], window_tokens=c["window"],
+                        last_n_blocks=c["last_n"], mean_correction=c["corr"])
+    total = lk if c["total"] else None
+    q, k, v = structured_qkv(length=lk, query_heads=hq, kv_heads=hkv, head_dim=d,
+                             block_size=c["block_k"], seed=c["seed"], dtype=dtype)
+    q = q[:, lk - lq:]
+    enable(config, min_tokens=1, collect_stats=True, total_tokens=total)
+    try:
+        qd, kd, vd = (x[None].to(cuda) for x in (q, k, v))
+        if lq == lk:
+            out = F.scaled_dot_product_attention(qd, kd, vd, is_causal=True, scale=c["scale"],
+                                                 enable_gqa=True)
+        else:
+            out = F.scaled_dot_product_attention(qd, kd, vd, attn_mask=causal_lower_right(lq, lk),
+                                                 scale=c["scale"], enable_gqa=True)
+        torch.cuda.synchronize()
+        # the FPV2 path ran (an ineligible call would be counted as dense)
+        assert patch._selected_dense_blocks == 0 and patch._visible_blocks > 0
+        sparsity = block_sparsity()
+    finally:
+        disable()
+
+    ocfg = orc.OracleConfig(**{f: getattr(config, f) for f in orc.OracleConfig.__dataclass_fields__})
+    ocfg = orc.request_config(ocfg, lk, total)
+    want, plan = orc.fpv2_sdpa_oracle(to_np(q), to_np(k), to_np(v), scale=c["scale"], config=ocfg,
+                                      dtype=_DT[dtype], return_plan=True)
+    got = to_np(out[0])
+    assert got.shape == want.shape and np.isfinite(got).all()
+    # rows of tiles where some block sits within the band around alpha may
+    # select differently on the device (float32 energies); compare the rest
+    tq = plan["config"].tile_q
+    near = (np.abs(plan["ratio"] - ocfg.alpha) <= BAND).any(axis=(0, 2))
+    rows = np.ones(lq, dtype=bool)
+    for t in np.nonzero(near)[0]:
+        rows[t * tq:(t + 1) * tq] = False
+    assert rows.mean() > 0.5
+    err = attention_errors(got[:, rows], want[:, rows])
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+    if not near.any():
+        # accounting: the device's selected count equals the oracle's
+        visible = orc.causal_block_count(hkv, lq, plan["offset"], plan["config"])
+        assert sparsity == 1.0 - int(plan["lists"][1].sum()) / visible
