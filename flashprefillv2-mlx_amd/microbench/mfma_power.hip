@@ -17,9 +17,13 @@
 //   16x16x32 constant / random           80-81 % at 1.98-2.01 GHz
 //   32x32x16 random + the slice's VALU   58.2-58.5 % at 1.98 GHz
 //   16x16x32 random + the slice's VALU   60.1-60.2 % at 2.30 GHz
+//   32x32x16 f16 random                  68.1-68.2 % at 1.73-1.74 GHz
+//   32x32x16 f16 random + slice VALU     55.5-55.7 % at 1.89-1.90 GHz
+//     (bf16 in the same runs: 69.8-70.4 %, and 57.1 % at 1.94-1.95 GHz)
 // The chip is power-limited with the matrix pipe full: the 16x16x32 shape
 // draws less power per FLOP and runs 13 % faster, random operands cost
-// about 1 %.  With the VALU work interleaved the 16x16x32 loop runs at a
+// about 1 %, and the f16 MFMA about 3 % more than the bf16 one (its
+// operands here carry bf16's 8 significant bits).  With the VALU work interleaved the 16x16x32 loop runs at a
 // higher clock but keeps the pipe busy for fewer of its cycles (63 % against
 // 71 %), and the difference shrinks to 3 %.
 //
@@ -75,7 +79,10 @@ __device__ __forceinline__ void slice_valu_half(float (&x)[8], uint32_t& w, floa
   if (k < 5) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(adr) : "v"(x[k]));
 }
 
-// SHAPE 0: 32x32x16 (4 chains), 1: 16x16x32 (8 chains).  RANDOM: cycle 8
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// SHAPE 0: 32x32x16 (4 chains), 1: 16x16x32 (8 chains), 2: 32x32x16 f16
+// (v_mfma_f32_32x32x16_f16, operands converted from the same random data).  RANDOM: cycle 8
 // operand pairs of random data, else one constant pair.  MIX: the attention
 // slice's VALU work (slice_valu_half per 8 32x32x16-equivalents) interleaved
 // with the MFMAs in the same wave.
@@ -104,6 +111,27 @@ __global__ __launch_bounds__(512) void mfma_loop(float* out, unsigned long long*
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[k], b[k], acc[k & 3], 0, 0, 0);
+        if constexpr (MIX) slice_valu_half(x, w, l, adr, k);
+      }
+    }
+    c1 = __builtin_amdgcn_s_memtime();
+    t1 = __builtin_amdgcn_s_memrealtime();
+    for (int c = 0; c < 4; ++c)
+      for (int i = 0; i < 16; ++i) r += acc[c][i];
+  } else if constexpr (SHAPE == 2) {
+    f16x8 ah[8], bh[8];
+    for (int p = 0; p < 8; ++p)
+      for (int i = 0; i < 8; ++i) {
+        ah[p][i] = (_Float16)(float)a[p][i];
+        bh[p][i] = (_Float16)(float)b[p][i];
+      }
+    f32x16 acc[4] = {};
+    t0 = __builtin_amdgcn_s_memrealtime();
+    c0 = __builtin_amdgcn_s_memtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc[k & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[k], bh[k], acc[k & 3], 0, 0, 0);
         if constexpr (MIX) slice_valu_half(x, w, l, adr, k);
       }
     }
@@ -180,6 +208,8 @@ int main() {
     if (run<1, true>(ncu, out, ticks, "16x16x32 random")) return 1;
     if (run<0, true, true>(ncu, out, ticks, "32x32x16 random + VALU")) return 1;
     if (run<1, true, true>(ncu, out, ticks, "16x16x32 random + VALU")) return 1;
+    if (run<2, true>(ncu, out, ticks, "32x32x16 f16 random")) return 1;
+    if (run<2, true, true>(ncu, out, ticks, "32x32x16 f16 rnd + VALU")) return 1;
   }
   CHECK(hipFree(out));
   CHECK(hipFree(ticks));
