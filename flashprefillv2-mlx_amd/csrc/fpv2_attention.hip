@@ -758,11 +758,14 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
     // (elements 8-15) for the partner's partial of ours, added to elements
     // 0-7, and the P of the pending slice's own keys for the partner's P,
     // the second P operand of stage B.  Every wave of the workgroup takes
-    // this path in the same calls, so the barrier is uniform; the next write
-    // follows the next sub-tile's barrier, after the partner's reads.
+    // this path in the same calls, so the barriers are uniform.  A wave
+    // writes its area only after a barrier that follows the partner's reads
+    // of the previous contents: the sub-tile's barrier, or for the call of
+    // the walk's last pending slice (no sub-tile), the barrier below.
     if constexpr ((HN || HP) && KSPLIT) {
       uint8_t* const mine = xbuf + wave * 4096;
       const uint8_t* const theirs = xbuf + (wave ^ (WAVES / 2)) * 4096;
+      if constexpr (!HN) barrier_lds();
       if constexpr (HN) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
