@@ -12,14 +12,16 @@
 //     packed rows (row = g*tile_q + p) share the block lists, so the G query
 //     heads of a KV head share every K/V load.  A workgroup has 4 waves
 //     (128 rows, two workgroups per CU); D = 256 uses 8 waves for the same
-//     rows, two per 32-row group, each owning half of the head dimension;
+//     rows, two per 32-row group, each owning half of the head dimension
+//     for the products and half of each slice's keys for the softmax;
 //   * each wave owns 32 query rows; Q lives in VGPRs for the whole walk;
 //   * S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: lane l owns query
 //     row l%32 and 16 of the 32 keys of each key tile, so row max/sum need a
 //     single lane-pair exchange and P feeds the next MFMA without a transpose;
 //   * O^T = V^T . P^T: the rescale by exp2(m_old - m_new) is lane-local;
-//   * K/V sub-tiles of 32 keys stream through a ring of NST LDS stages filled
-//     by buffer_load_dwordx4 ... lds, NST-2 sub-tiles ahead of the multiply; LDS rows are unpadded with an XOR swizzle of their
+//   * K/V sub-tiles of 32 keys stream through a ring of NST LDS stages
+//     filled by buffer_load_dwordx4 ... lds, NST-2 sub-tiles ahead of the
+//     multiply; LDS rows are unpadded with an XOR swizzle of their
 //     16-byte chunks, so K (ds_read_b128) and V (ds_read_b64_tr_b16, which
 //     transposes on the way out) are read without bank conflicts and every
 //     wave issues the same number of fills per stage;
