@@ -50,25 +50,41 @@ class SelectedBlockCounter:
     kept rather than reduced: every ``fold_every`` calls the kept tensors are
     summed by one concatenation and one reduction into a 0-d int64 device
     total, so a call launches no kernel and nothing synchronises until
-    ``value()`` is read.
+    ``value()`` is read.  Each kept tensor remembers the stream that wrote
+    it; the stream that folds waits for those streams first.
     """
 
     def __init__(self, fold_every: int = 64) -> None:
         self.fold_every = fold_every
         self._pending: list[torch.Tensor] = []
+        self._streams: list[torch.cuda.Stream] = []
         self._total: torch.Tensor | None = None
 
     def add(self, counts: torch.Tensor) -> None:
         self._pending.append(counts)
+        if counts.is_cuda:
+            stream = torch.cuda.current_stream(counts.device)
+            if all(stream != s for s in self._streams):
+                self._streams.append(stream)
         if len(self._pending) >= self.fold_every:
             self._fold()
 
     def _fold(self) -> None:
         if not self._pending:
             return
+        if self._streams:
+            current = torch.cuda.current_stream(self._pending[0].device)
+            for stream in self._streams:
+                if stream != current:
+                    current.wait_stream(stream)
+            # the allocator must not reuse a kept tensor's memory on its own
+            # stream before this stream has read it
+            for c in self._pending:
+                c.record_stream(current)
         part = torch.cat([c.reshape(-1) for c in self._pending]).sum(dtype=torch.int64)
         self._total = part if self._total is None else self._total + part
         self._pending.clear()
+        self._streams = [torch.cuda.current_stream(part.device)] if part.is_cuda else []
 
     def device_total(self) -> torch.Tensor | None:
         """The sum so far as a 0-d int64 device tensor (None if nothing was
@@ -83,6 +99,7 @@ class SelectedBlockCounter:
 
     def reset(self) -> None:
         self._pending.clear()
+        self._streams.clear()
         self._total = None
 
 

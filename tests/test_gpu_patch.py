@@ -183,3 +183,22 @@ def test_baseline_contrast_variant_exercises_pruning(cuda):
     dens = orc.density(plan["selected"], config=plan["config"])
     assert dens < 0.6  # real pruning, so the pooled correction is active
     assert int(plan["lists"][3].max()) > 0
+
+
+def test_block_counter_waits_for_the_stream_that_wrote_the_counts(cuda):
+    """Counts written on a side stream (behind a long matmul) are summed on
+    the default stream: the fold waits for the side stream."""
+    from fpv2.patch import SelectedBlockCounter
+    counter = SelectedBlockCounter(fold_every=4)
+    side = torch.cuda.Stream(device=cuda)
+    a = torch.randn((4096, 4096), device=cuda)
+    torch.cuda.synchronize()
+    expected = 0
+    with torch.cuda.stream(side):
+        for i in range(6):
+            b = a @ a  # keeps the side stream busy before each count is written
+            counts = torch.full((2, 8), i + 1, dtype=torch.int32, device=cuda)
+            counts += (b[0, :1] * 0).to(torch.int32)  # written after the matmul
+            counter.add(counts)
+            expected += 16 * (i + 1)
+    assert counter.value() == expected
