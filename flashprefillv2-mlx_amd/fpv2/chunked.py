@@ -28,6 +28,10 @@ With ``collect_stats`` the layer counts selected and visible blocks as the
 hook's ``block_sparsity`` does (``patch.py:66-88``): selected counts are kept
 on the device and summed in batches (``SelectedBlockCounter``), and
 ``block_sparsity()`` synchronises once to read them.
+
+Every call runs on the current stream.  As with a module's buffers, the KV
+and pooled caches are not synchronised across streams: a caller that moves
+between streams orders the calls itself (``wait_stream``).
 """
 
 from __future__ import annotations
