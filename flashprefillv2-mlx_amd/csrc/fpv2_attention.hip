@@ -91,37 +91,6 @@ __device__ __forceinline__ float pair_sum(float x) {
 }
 
 
-// O accumulators in AGPRs (the RG = 2 shape): the PV MFMA as inline asm
-// with its C/D operand constrained to AGPRs.  The compiler does not know the
-// asm is an MFMA and inserts no wait states for it, so the code around it
-// supplies them:
-//   * P and V^T operands: the two wait states a VALU write needs before an
-//     MFMA reads the register (the s_nop 1 in front of each MFMA);
-//   * accumulator chains: back-to-back MFMAs on the same C/D registers need
-//     none;
-//   * AGPR reads by VALU (rescale, epilogue) and AGPR writes followed by an
-//     MFMA: agpr_fence(), which names the accumulators as asm operands so no
-//     read or write of them can move across it.
-template <typename T> __device__ __forceinline__ void mfma_agpr(f32x16& acc, u32x4 a, u32x4 b);
-template <> __device__ __forceinline__ void mfma_agpr<bf16_t>(f32x16& acc, u32x4 a, u32x4 b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-template <> __device__ __forceinline__ void mfma_agpr<f16_t>(f32x16& acc, u32x4 a, u32x4 b) {
-  asm volatile("s_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
-}
-// 24 wait states: covers the latency of an in-flight 32x32 MFMA before its
-// accumulators are read by VALU, and VALU writes of them before an MFMA.
-template <int DT>
-__device__ __forceinline__ void agpr_fence(f32x16 (&o)[DT]) {
-  static_assert(DT >= 2 && DT <= 4, "2 to 4 accumulator tiles");
-  if constexpr (DT == 2)
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]));
-  else if constexpr (DT == 3)
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]));
-  else
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]));
-}
-
 struct AttnArgs {
   const uint16_t* q;
   const uint16_t* k;
@@ -198,14 +167,13 @@ struct Step {
 // softmax work is not repeated.  Each accumulates its half of O from both
 // halves of P.  This keeps D = 256 at two waves per SIMD within 256
 // registers.
-// RG = 2: a wave owns two 32-row groups that share every K/V fragment read
-// from LDS; with the whole 512-entry register file of its SIMD (one wave per
-// SIMD) the two groups' matrix and softmax work interleave within the wave.
-template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1, int RG = 1>
-__global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ? 2 : 1))) void sparse_attn_kernel(AttnArgs a) {
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
+__global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D>;
   static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0), "D split in halves");
-  static_assert(RG == 1 || (RG == 2 && DS == 1), "two row groups per wave without the D split");
+  // 32-row groups per wave: one.  The per-row-group arrays below keep the
+  // row group as their first index.
+  constexpr int RG = 1;
   // asm LDS reads unless a wave's registers do not hold them (D = 256 without
   // the split), where the compiler schedules its LDS reads (see lds_read_b128).
   constexpr bool kAsm = D <= 128 || DS == 2;
@@ -521,13 +489,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // common case costs no rescale at all.  The result O / l is unchanged.
   constexpr float kRescaleSlack = 8.0f;
   f32x16 o[RG][DT];
-  // RG = 2: O lives in AGPRs, accumulated by inline-asm MFMAs (mfma_agpr)
-  constexpr bool kAccA = RG == 2;
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
 #pragma unroll
     for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
-    if constexpr (kAccA) agpr_fence(o[rg]);
   }
   float m_ref[RG];
   // Derived from m_ref, updated only when it changes: the exp2 bias
@@ -835,8 +800,7 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
 #pragma unroll
             for (int rg = 0; rg < RG; ++rg) {
-              if constexpr (kAccA) mfma_agpr<T>(o[rg][dt], av, __builtin_bit_cast(u32x4, pb[rg][u]));
-              else o[rg][dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[rg][u], o[rg][dt]);
+              o[rg][dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[rg][u], o[rg][dt]);
             }
             if constexpr (EB < NP && op < DT) {
               StaticFor<EB + op * (NP - EB) / DT, EB + (op + 1) * (NP - EB) / DT>::run(exp_pair);
@@ -892,10 +856,8 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
             m_thr[rg] = m_ref[rg] + kRescaleSlack;
           }
           l_run[rg] *= alpha;
-          if constexpr (kAccA) agpr_fence(o[rg]);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) scale_in_place(o[rg][dt], alpha);
-          if constexpr (kAccA) agpr_fence(o[rg]);
         }
       }
     }
@@ -1007,10 +969,8 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   if (redo) {
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
-      if constexpr (kAccA) agpr_fence(o[rg]);
 #pragma unroll
       for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
-      if constexpr (kAccA) agpr_fence(o[rg]);
       m_ref[rg] = neg_inf();
       neg_m[rg] = 0.f;
       m_thr[rg] = neg_inf();
@@ -1029,7 +989,6 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   // ---- normalise and store ----
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
-    if constexpr (kAccA) agpr_fence(o[rg]);
     const float l_tot = row_sum(rg);
     if (!exists[rg] || pos[rg] >= a.out_rows) continue;
     const float inv = (row_valid[rg] && l_tot > 0.f) ? 1.f / l_tot : 0.f;
@@ -1048,10 +1007,10 @@ __global__ __launch_bounds__(WAVES * 64, (RG == 2 ? 1 : ((D <= 128 || DS == 2) ?
   }
 }
 
-template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1, int RG = 1>
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
 int launch_attn(AttnArgs a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS, RG>;
-  constexpr int RW = WAVES / DS * 32 * RG;
+  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS>;
+  constexpr int RW = WAVES / DS * 32;
   a.nchunk = (a.G * a.tq + RW - 1) / RW;
   const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
   if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
@@ -1065,14 +1024,9 @@ int launch_attn(AttnArgs a, hipStream_t stream) {
 // between 256 rows, was measured no faster at 512-row tiles and up to 17 %
 // slower at 256-row tiles.)  D = 256: 8 waves for 128 rows, two per 32-row
 // group each owning half of D (DS = 2), 160 KiB.
-#ifndef FPV2_ROW_GROUPS
-#define FPV2_ROW_GROUPS 1
-#endif
 template <typename T, int D, bool CORR>
 int launch_shape(const AttnArgs& a, hipStream_t s) {
-  if constexpr (D <= 128 && FPV2_ROW_GROUPS == 2) {
-    return launch_attn<T, D, CORR, 2, 4, 1, 2>(a, s);
-  } else if constexpr (D <= 128) {
+  if constexpr (D <= 128) {
     return launch_attn<T, D, CORR, 4, 4>(a, s);
   } else {
     return launch_attn<T, D, CORR, 8, 4, 2>(a, s);
