@@ -623,11 +623,7 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(1, 
   };
   // the same by inline-asm reads: fragment k of group RG at a fixed offset
   // from the lane's row of group 0
-#ifndef FPV2_SEL_KPRE
-#define FPV2_SEL_KPRE 0
-#endif
   constexpr bool kResident = D <= 128;  // Q of the pass held in registers
-  constexpr bool kPrefetch = FPV2_SEL_KPRE != 0 && D <= 128;
   const uint32_t qaddr = lds_addr(qrow);
   auto read_q = [&](auto rgc, u32x4 (&qf)[KS]) {
     constexpr int rg = decltype(rgc)::value;
@@ -829,24 +825,11 @@ __global__ __launch_bounds__(kThreads, 2) __attribute__((amdgpu_waves_per_eu(1, 
       if (all_full && min_lo >= lo_last) chunk_fast(c, kf);
       else chunk_gen(c, kf);
     };
-    // this wave's chunks c = wave + 4 i, pooled keys loaded one chunk ahead
-    // where registers allow a second set
-    if constexpr (kPrefetch) {
-      u32x4 ka[KS], kb[KS];
-      load_kbar(wave, ka);
-      for (int c = wave; c < nchunks; c += 8) {
-        load_kbar(c + 4, kb);
-        chunk(c, ka);
-        if (c + 4 >= nchunks) break;
-        load_kbar(c + 8, ka);
-        chunk(c + 4, kb);
-      }
-    } else {
-      for (int c = wave; c < nchunks; c += 4) {
-        u32x4 kf[KS];
-        load_kbar(c, kf);
-        chunk(c, kf);
-      }
+    // this wave's chunks c = wave + 4 i
+    for (int c = wave; c < nchunks; c += 4) {
+      u32x4 kf[KS];
+      load_kbar(c, kf);
+      chunk(c, kf);
     }
   }
   // common reference: every wave rescales the blocks it owns by 2^(m_w - G)
