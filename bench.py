@@ -17,7 +17,9 @@ Reported beside it (each a BASELINE config unless labelled otherwise):
 ``at_32k`` (config 2), ``at_32k_no_corr`` (its no-corr ablation),
 ``alpha_0.05`` / ``alpha_0.2`` (config 3's sweep), ``contrast_variant`` (the
 sparse regime: planted x 3*sqrt(D), most blocks pruned, correction phase
-active; labelled supplementary), ``chunked_64k`` (config 4), and
+active; labelled supplementary), ``kv_head_share`` (one GPU's share of the
+primary layer under KV-head sharding: one KV head and its query heads),
+``chunked_64k`` (config 4), and
 ``e2e_qwen3_4b_64k`` (config 5: prefill tok/s and time to first token, FPV2
 vs dense vs stock; ``prefill_tok_per_s`` / ``ttft_s`` at the top level).
 ``stock_sdpa`` (and ``at_32k.stock_sdpa``) times PyTorch-ROCm's fused flash
@@ -106,8 +108,8 @@ def profiled_traffic(seq: int, alpha: float):
     return None, None
 
 
-def dense_flops(seq: int) -> int:
-    return 4 * D * HQ * seq * (seq + 1) // 2
+def dense_flops(seq: int, query_heads: int = HQ) -> int:
+    return 4 * D * query_heads * seq * (seq + 1) // 2
 
 
 def heavy_fraction(seq: int) -> float:
@@ -116,7 +118,7 @@ def heavy_fraction(seq: int) -> float:
 
 
 def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, corr=True,
-               seed=0):
+               seed=0, query_heads=HQ, kv_heads=HKV):
     from fpv2 import FPV2Config
     from fpv2.patch import _fpv2_sdpa
     from fpv2.synthetic import baseline_qkv
@@ -124,7 +126,8 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
     dev = torch.device("cuda:0")
     heavy = heavy_fraction(seq) if heavy is None else heavy
     log(f"seq {seq}: generating inputs (planted {planted:.2f}, heavy {heavy})")
-    q, k, v = baseline_qkv(seq, planted=planted, heavy_fraction=heavy, seed=seed, device=dev)
+    q, k, v = baseline_qkv(seq, query_heads=query_heads, kv_heads=kv_heads, planted=planted,
+                           heavy_fraction=heavy, seed=seed, device=dev)
     q4, k4, v4 = q[None], k[None], v[None]
     config = FPV2Config(alpha=alpha, sink_tokens=BLOCK, mean_correction=corr)
     scale = D ** -0.5
@@ -158,11 +161,13 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
     out = _fpv2_sdpa(q4, k4, v4, scale=scale, config=config, keep=keep)
     torch.cuda.synchronize()
     f_ret, sel_frac = retained_flops(keep, seq, torch)
-    f_dense = dense_flops(seq)
+    f_dense = dense_flops(seq, query_heads)
     nb = keep["lists"][0].shape[-1]
-    pool_bytes = 2 * HKV * seq * D * 2 + 2 * HKV * nb * D * 2
+    pool_bytes = 2 * kv_heads * seq * D * 2 + 2 * kv_heads * nb * D * 2
     res = {
         "seq": seq,
+        "query_heads": query_heads,
+        "kv_heads": kv_heads,
         "alpha": alpha,
         "mean_correction": corr,
         "planted": planted,
@@ -505,6 +510,13 @@ def main(argv=None) -> int:
                       "direction x 3*sqrt(D) so most blocks are pruned and the correction "
                       "phase carries the pruned blocks' pooled rows")
         extra["contrast_variant"] = c
+        torch.cuda.empty_cache()
+        # one GPU's share of the primary layer under 8-way KV-head sharding
+        share, _ = run_config(torch, args.seq, args.alpha, x_steps, x_warm,
+                              query_heads=HQ // HKV, kv_heads=1)
+        share["label"] = ("one GPU's share of the primary layer under KV-head sharding over "
+                          f"{HKV} GPUs (Hq {HQ // HKV}, Hkv 1; design only, no collective runs)")
+        extra["kv_head_share"] = share
         torch.cuda.empty_cache()
         extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
         torch.cuda.empty_cache()
