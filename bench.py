@@ -465,8 +465,9 @@ def main(argv=None) -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures a single MI355X: the FPV2 path runs on one GPU in this "
-              "build (KV-head sharding across GPUs is described in DESIGN.md but not "
-              "launched); run with --gpus 1", file=sys.stderr)
+              "build (KV-head sharding across GPUs is designed but not launched; the "
+              "kv_head_share field reports one GPU's share); run with --gpus 1",
+              file=sys.stderr)
         return 2
 
     import torch
