@@ -202,3 +202,31 @@ def test_block_counter_waits_for_the_stream_that_wrote_the_counts(cuda):
             counter.add(counts)
             expected += 16 * (i + 1)
     assert counter.value() == expected
+
+
+@pytest.mark.parametrize(("heads", "dim"), [((32, 2), 128), ((64, 2), 64), ((32, 1), 128)])
+def test_large_gqa_groups_match_oracle(cuda, heads, dim):
+    """G = 16 and 32 query heads per KV head: the hook's 128 packed rows
+    become tiles of 8 and 4 query positions (patch.py:41-52)."""
+    hq, hkv = heads
+    lq = lk = 1536
+    q, k, v = structured_qkv(length=lk, query_heads=hq, kv_heads=hkv, head_dim=dim, seed=hq + dim,
+                             dtype=torch.bfloat16)
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=128)
+    scale = dim ** -0.5
+    # the whole request in one call: the dense tail applies (patch.py:55-63)
+    enable(config, min_tokens=1, total_tokens=lk)
+    out = _hook_call(q[None].to(cuda), k[None].to(cuda), v[None].to(cuda), scale)[0]
+    torch.cuda.synchronize()
+    want, plan = orc.fpv2_sdpa_oracle(to_np(q), to_np(k), to_np(v), scale=scale,
+                                      config=orc.OracleConfig(alpha=0.15, sink_tokens=128,
+                                                              window_tokens=128),
+                                      return_plan=True)
+    assert plan["config"].tile_q == 128 // (hq // hkv)
+    tq = plan["config"].tile_q
+    near = (np.abs(plan["ratio"] - 0.15) <= 1e-4).any(axis=(0, 2))
+    rows = np.ones(lq, dtype=bool)
+    for t in np.nonzero(near)[0]:
+        rows[t * tq:(t + 1) * tq] = False
+    err = attention_errors(to_np(out)[:, rows], want[:, rows])
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
