@@ -67,6 +67,26 @@ def _id(c: dict) -> str:
 
 @pytest.mark.parametrize("c", CASES, ids=[_id(c) for c in CASES])
 def test_random_configuration_matches_oracle(cuda, c):
+    _check_operators(cuda, c)
+
+
+# Block sizes that are not a power of two or exceed the 32-key sub-tile
+# (the last sub-tile of every block is partial for 48 and 96).
+ODD_BLOCKS = [
+    dict(case=100 + i, head_dim=d, dtype=torch.bfloat16, kv_heads=2, query_heads=8, block_k=bk,
+         tile_q=tq, alpha=0.15, sink=bk, window=2 * bk, last_n=1, corr=True, offset=off,
+         qlen=ql, sign=1.0, seed=7 + i)
+    for i, (d, bk, tq, off, ql) in enumerate([(128, 48, 16, 0, 600), (64, 96, 32, 130, 500),
+                                              (128, 256, 64, 0, 1100), (256, 48, 32, 77, 420),
+                                              (96, 256, 16, 300, 700)])]
+
+
+@pytest.mark.parametrize("c", ODD_BLOCKS, ids=[_id(c) for c in ODD_BLOCKS])
+def test_block_sizes_off_the_sub_tile_grid_match_oracle(cuda, c):
+    _check_operators(cuda, c)
+
+
+def _check_operators(cuda, c):
     d, dtype, bk, tq = c["head_dim"], c["dtype"], c["block_k"], c["tile_q"]
     hq, hkv, offset, qlen = c["query_heads"], c["kv_heads"], c["offset"], c["qlen"]
     config = FPV2Config(block_k=bk, tile_q=tq, alpha=c["alpha"], sink_tokens=c["sink"],
