@@ -50,6 +50,27 @@ def test_chunked_matches_hook_bit_exact(cuda, total, chunk):
     assert cp.pooled_rows == total - total % 128 + partial
 
 
+@pytest.mark.parametrize(("dtype", "d", "heads"), [(torch.float16, 128, (8, 2)),
+                                                  (torch.bfloat16, 64, (16, 2)),
+                                                  (torch.float16, 256, (4, 1)),
+                                                  (torch.bfloat16, 96, (6, 3))])
+def test_chunked_other_dtypes_and_head_dims_match_hook_bit_exact(cuda, dtype, d, heads):
+    hq, hkv = heads
+    total, chunk = 2304, 700
+    q, k, v = structured_qkv(length=total, query_heads=hq, kv_heads=hkv, head_dim=d, seed=d + hq)
+    q, k, v = (x.to(dtype).to(cuda) for x in (q, k, v))
+    config = FPV2Config(alpha=0.15, sink_tokens=128, window_tokens=256)
+    cp = ChunkedPrefill(hq, hkv, d, total, config=config, total_tokens=total, min_tokens=1,
+                        dtype=dtype, device=cuda)
+    for start in range(0, total, chunk):
+        end = min(start + chunk, total)
+        out = cp.step(q[:, start:end], k[:, start:end], v[:, start:end])
+        ref = fpv2_sdpa(q[None, :, start:end], k[None, :, :end], v[None, :, :end],
+                        scale=d ** -0.5, config=cp.request_config())
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), (start, end)
+
+
 def test_dense_tail_only_at_total_tokens(cuda):
     cp = ChunkedPrefill(8, 2, 128, 4096, total_tokens=4096, min_tokens=1, device=cuda)
     q, k, v = _inputs(cuda, 4096)
