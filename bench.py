@@ -19,7 +19,9 @@ Reported beside it (each a BASELINE config unless labelled otherwise):
 sparse regime: planted x 3*sqrt(D), most blocks pruned, correction phase
 active; labelled supplementary), ``kv_head_share`` (one GPU's share of the
 primary layer under KV-head sharding: one KV head and its query heads),
-``chunked_64k`` (config 4), and
+``chunked_64k`` (config 4; ``chunked_64k_contrast`` on the contrast
+generator), ``other_geometries_32k`` (config 2's layer at head_dim 64, 96,
+256 and in float16), and
 ``e2e_qwen3_4b_64k`` (config 5: prefill tok/s and time to first token, FPV2
 vs dense vs stock; ``prefill_tok_per_s`` / ``ttft_s`` at the top level).
 ``stock_sdpa`` (and ``at_32k.stock_sdpa``) times PyTorch-ROCm's fused flash
@@ -55,7 +57,7 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def retained_flops(keep, seq, torch):
+def retained_flops(keep, seq, torch, head_dim=D, group=HQ // HKV):
     """Algorithmic FLOPs of the attention kernel for one layer.
 
     4*D*G per (query row, visited key): QK^T and PV, 2 FLOPs per MAC.  Exact
@@ -84,8 +86,7 @@ def retained_flops(keep, seq, torch):
         exact += int((vis * per_tile[t0:t1]).sum().item())
     rows_per_tile = torch.clamp(seq - torch.arange(nt, device=dev) * tq, 0, tq)
     corr = int((pcounts.long() * rows_per_tile[None, :]).sum().item()) if cfg.mean_correction else 0
-    group = HQ // HKV
-    return 4 * D * group * (exact + corr), float(mask.float().mean().item())
+    return 4 * head_dim * group * (exact + corr), float(mask.float().mean().item())
 
 
 def profiled_traffic(seq: int, alpha: float):
@@ -108,8 +109,8 @@ def profiled_traffic(seq: int, alpha: float):
     return None, None
 
 
-def dense_flops(seq: int, query_heads: int = HQ) -> int:
-    return 4 * D * query_heads * seq * (seq + 1) // 2
+def dense_flops(seq: int, query_heads: int = HQ, head_dim: int = D) -> int:
+    return 4 * head_dim * query_heads * seq * (seq + 1) // 2
 
 
 def heavy_fraction(seq: int) -> float:
@@ -118,7 +119,7 @@ def heavy_fraction(seq: int) -> float:
 
 
 def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, corr=True,
-               seed=0, query_heads=HQ, kv_heads=HKV):
+               seed=0, query_heads=HQ, kv_heads=HKV, head_dim=D, dtype=None):
     from fpv2 import FPV2Config
     from fpv2.patch import _fpv2_sdpa
     from fpv2.synthetic import baseline_qkv
@@ -126,11 +127,13 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
     dev = torch.device("cuda:0")
     heavy = heavy_fraction(seq) if heavy is None else heavy
     log(f"seq {seq}: generating inputs (planted {planted:.2f}, heavy {heavy})")
-    q, k, v = baseline_qkv(seq, query_heads=query_heads, kv_heads=kv_heads, planted=planted,
-                           heavy_fraction=heavy, seed=seed, device=dev)
+    dtype = torch.bfloat16 if dtype is None else dtype
+    q, k, v = baseline_qkv(seq, query_heads=query_heads, kv_heads=kv_heads, head_dim=head_dim,
+                           planted=planted, heavy_fraction=heavy, seed=seed, dtype=dtype,
+                           device=dev)
     q4, k4, v4 = q[None], k[None], v[None]
     config = FPV2Config(alpha=alpha, sink_tokens=BLOCK, mean_correction=corr)
-    scale = D ** -0.5
+    scale = head_dim ** -0.5
     for _ in range(warmup):
         _fpv2_sdpa(q4, k4, v4, scale=scale, config=config)
     torch.cuda.synchronize()
@@ -160,14 +163,16 @@ def run_config(torch, seq, alpha, steps, warmup, *, planted=3.0, heavy=None, cor
     keep = {}
     out = _fpv2_sdpa(q4, k4, v4, scale=scale, config=config, keep=keep)
     torch.cuda.synchronize()
-    f_ret, sel_frac = retained_flops(keep, seq, torch)
-    f_dense = dense_flops(seq, query_heads)
+    f_ret, sel_frac = retained_flops(keep, seq, torch, head_dim, query_heads // kv_heads)
+    f_dense = dense_flops(seq, query_heads, head_dim)
     nb = keep["lists"][0].shape[-1]
-    pool_bytes = 2 * kv_heads * seq * D * 2 + 2 * kv_heads * nb * D * 2
+    pool_bytes = 2 * kv_heads * seq * head_dim * 2 + 2 * kv_heads * nb * head_dim * 2
     res = {
         "seq": seq,
         "query_heads": query_heads,
         "kv_heads": kv_heads,
+        "head_dim": head_dim,
+        "dtype": str(dtype).replace("torch.", ""),
         "alpha": alpha,
         "mean_correction": corr,
         "planted": planted,
@@ -244,47 +249,64 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def _host_workers() -> int:
+    """Threads for the CPU baseline: the cores this process may run on (at
+    most 16, the GPU box's CPU share)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def _device_mask(ids, counts, num_blocks):
+    import numpy as np
+    ids_np, counts_np = ids.cpu().numpy(), counts.cpu().numpy()
+    pos = np.arange(ids_np.shape[-1])
+    mask = np.zeros(ids_np.shape[:2] + (num_blocks,), dtype=bool)
+    h, t, j = np.nonzero(pos[None, None, :] < counts_np[..., None])
+    mask[h, t, ids_np[h, t, j]] = True
+    return mask
+
+
 def cpu_baseline(torch, data, seq, alpha, budget_s: float):
     """Oracle (numpy) selection and attention on the last tiles of the layer,
-    timed separately; the same tiles' device results are checked against it."""
+    timed separately on the host's cores (tile ranges on parallel threads),
+    with the same tiles' device results checked against it; the full
+    layer's CPU time extrapolated from them; and BASELINE config 1 (the
+    whole 8k layer, which the reference's CPU path runs) timed in full."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
 
     from oracle import fpv2_oracle as orc
 
     q, k, v, keep, out_dev = data
     cfg = keep["config"]
-    tq = cfg.tile_q
-    cores = len(os.sched_getaffinity(0))
+    tq, bk = cfg.tile_q, cfg.block_k
+    workers = _host_workers()
     ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
     pooled_k = keep["pooled_k"].float().cpu().numpy()
     pooled_v = keep["pooled_v"].float().cpu().numpy()
     kn = k.float().cpu().numpy()
     vn = v.float().cpu().numpy()
     nt = seq // tq
+    nb = pooled_k.shape[1]
+
+    def nvis(tiles):  # blocks each tile scores (those that start in its causal range)
+        last = np.minimum((np.asarray(tiles) + 1) * tq, seq) - 1
+        return np.minimum(nb, last // bk + 1)
 
     def sample(n_tiles):
         rows0 = seq - n_tiles * tq
         qs = q[:, rows0:].float().cpu().numpy()
         ids, counts, pids, pcounts = (x[:, nt - n_tiles:] for x in keep["lists"])
-        # the device's selection of the sampled tiles as a mask
-        ids_np, counts_np = ids.cpu().numpy(), counts.cpu().numpy()
-        dev_sel = np.zeros(ids_np.shape, dtype=bool)
-        for h in range(ids_np.shape[0]):
-            for t in range(ids_np.shape[1]):
-                dev_sel[h, t, ids_np[h, t, :counts_np[h, t]]] = True
-        with threadpool_limits(limits=cores):
-            t0 = time.perf_counter()
-            sel, _, ratio = orc.block_scores_and_select(
-                qs, pooled_k, scale=D ** -0.5, config=orc._replace(ocfg, score_chunk_tiles=1),
-                offset=rows0, query_length=n_tiles * tq, return_ratio=True)
-            t1 = time.perf_counter()
-            # attention for the sampled rows on the device's selection (the same
-            # work as on the oracle's own), so the output compares like for like
-            out = orc.fpv2_attention_blockwise(
-                qs, kn, vn, scale=D ** -0.5, selected=dev_sel, pooled_k=pooled_k,
-                pooled_v=pooled_v, config=ocfg, offset=rows0, row_block=tq)
-            t2 = time.perf_counter()
+        dev_sel = _device_mask(ids, counts, nb)
+        t0 = time.perf_counter()
+        sel, ratio = orc.select_tile_ranges(qs, pooled_k, scale=D ** -0.5, config=ocfg,
+                                            offset=rows0, query_length=n_tiles * tq,
+                                            workers=workers, chunk_tiles=1)
+        t1 = time.perf_counter()
+        # attention for the sampled rows on the device's selection (the same
+        # work as on the oracle's own), so the output compares like for like
+        out = orc.attention_tile_ranges(qs, kn, vn, scale=D ** -0.5, selected=dev_sel,
+                                        pooled_k=pooled_k, pooled_v=pooled_v, config=ocfg,
+                                        offset=rows0, workers=workers, row_block=tq)
+        t2 = time.perf_counter()
         sub = dict(keep, offset=rows0, lists=(ids, counts, pids, pcounts))
         flops, _ = retained_flops(sub, n_tiles * tq, torch)
         decided = np.abs(ratio - cfg.alpha) > 1e-4
@@ -302,50 +324,147 @@ def cpu_baseline(torch, data, seq, alpha, budget_s: float):
                           and parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3)
         return t1 - t0, t2 - t1, flops, parity
 
-    s1, a1, _, _ = sample(1)
-    n = max(1, min(nt, int(budget_s / max(s1 + a1, 1e-3))))
-    log(f"cpu baseline: 1 tile took {s1 + a1:.2f} s; timing the last {n} tiles")
+    s1, a1, _, _ = sample(workers)
+    per_tile = (s1 + a1) / workers
+    n = max(workers, min(nt, int(budget_s / max(per_tile, 1e-3))))
+    log(f"cpu baseline: {workers} tiles took {s1 + a1:.2f} s on {workers} threads; "
+        f"timing the last {n} tiles")
     sel_s, attn_s, flops, parity = sample(n)
     log(f"parity of the sampled tiles against the oracle: {json.dumps(parity)}")
+    # the whole layer, extrapolated: attention by retained FLOPs, selection by
+    # scored (tile, block) pairs
+    f_full, _ = retained_flops(keep, seq, torch)
+    scored_full = float(nvis(np.arange(nt)).sum())
+    scored_sample = float(nvis(np.arange(nt - n, nt)).sum())
+    full = {
+        "label": "extrapolated from the timed sample (not run)",
+        "selection_s": sel_s * scored_full / scored_sample,
+        "attention_s": attn_s * f_full / flops,
+    }
+    full["layer_s"] = full["selection_s"] + full["attention_s"]
+    log(f"cpu baseline, full seq-{seq} layer (extrapolated): {full['layer_s']:.1f} s")
+    config1 = cpu_config1(torch, workers)
     return {
         "value": flops / (sel_s + attn_s) / 1e12,
         "unit": "TFLOP/s",
-        "cores": cores,
+        "cores": workers,
         "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": (f"numpy oracle (float64 selection, float32 attention with BLAS matmuls on "
-                   f"{cores} threads) of the last {n} query tiles ({n * tq} rows x {HQ} heads) "
-                   f"of the seq-{seq} alpha-{alpha} layer: selection {sel_s:.2f} s, attention "
-                   f"{attn_s:.2f} s for {flops:.3e} retained FLOP"),
+        "sample": (f"numpy oracle (float64 selection, float32 attention with BLAS matmuls; "
+                   f"tile ranges on {workers} threads) of the last {n} query tiles ({n * tq} "
+                   f"rows x {HQ} heads) of the seq-{seq} alpha-{alpha} layer: selection "
+                   f"{sel_s:.2f} s, attention {attn_s:.2f} s for {flops:.3e} retained FLOP"),
         "selection_s": sel_s,
         "attention_s": attn_s,
         "attention_tflops": flops / attn_s / 1e12,
         "selection_ms_per_tile": sel_s * 1e3 / n,
         "attention_ms_per_tile": attn_s * 1e3 / n,
         "parity": parity,
+        "full_layer_extrapolated": full,
+        "config1_8k": config1,
     }
 
 
-def run_chunked(torch, total: int, chunk: int, alpha: float):
+def cpu_config1(torch, workers):
+    """BASELINE config 1 (seq 8192, Qwen3-4B geometry, alpha 0.1, 1 sink block
+    + 3 local blocks + diagonal, last 2 tiles dense, correction on): the whole
+    layer through the oracle's hook data flow on the host's cores -- pooling,
+    selection, attention, each timed -- and compared with the device's hook
+    on the same inputs: pooled K/V and every tile's lists bit for bit (lists
+    outside the 1e-4 band), all rows within max-abs 2e-2 / mean-abs 2e-3."""
+    import numpy as np
+
+    from fpv2 import FPV2Config
+    from fpv2.patch import _fpv2_sdpa
+    from fpv2.synthetic import baseline_qkv
+    from oracle import fpv2_oracle as orc
+
+    seq = 8192
+    dev = torch.device("cuda:0")
+    q, k, v = baseline_qkv(seq, planted=3.0, heavy_fraction=0.06, seed=0, device=dev)
+    config = FPV2Config(alpha=0.1, sink_tokens=BLOCK)
+    keep = {}
+    out = _fpv2_sdpa(q[None], k[None], v[None], scale=D ** -0.5, config=config, keep=keep)
+    torch.cuda.synchronize()
+    cfg = keep["config"]
+    ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
+    qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
+    t0 = time.perf_counter()
+    pk = orc.pool_blocks(kn, BLOCK, out_dtype="bf16")
+    pv = orc.pool_blocks(vn, BLOCK, out_dtype="bf16")
+    t1 = time.perf_counter()
+    sel, ratio = orc.select_tile_ranges(qn, pk, scale=D ** -0.5, config=ocfg, workers=workers)
+    t2 = time.perf_counter()
+    ids, counts, pids, pcounts = keep["lists"]
+    dev_sel = _device_mask(ids, counts, ids.shape[-1])
+    ref = orc.attention_tile_ranges(qn, kn, vn, scale=D ** -0.5, selected=dev_sel,
+                                    pooled_k=pk, pooled_v=pv, config=ocfg, workers=workers)
+    t3 = time.perf_counter()
+    decided = np.abs(ratio - cfg.alpha) > 1e-4
+    o_ids, o_counts, o_pids, o_pcounts = orc.compact_block_indices(
+        dev_sel, config=ocfg, query_length=seq, key_length=seq)
+    head = np.arange(ids.shape[-1])[None, None, :] < o_pcounts[..., None]
+    lists_equal = (np.array_equal(ids.cpu().numpy(), o_ids)
+                   and np.array_equal(counts.cpu().numpy(), o_counts)
+                   and np.array_equal(pcounts.cpu().numpy(), o_pcounts)
+                   and np.array_equal(np.where(head, pids.cpu().numpy(), -1),
+                                      np.where(head, o_pids, -1)))
+    diff = np.abs(out[0].float().cpu().numpy().astype(np.float64) - ref)
+    pooled_equal = (np.array_equal(keep["pooled_k"].float().cpu().numpy(), pk)
+                    and np.array_equal(keep["pooled_v"].float().cpu().numpy(), pv))
+    flops, _ = retained_flops(keep, seq, torch)
+    parity = {
+        "tiles": int(ids.shape[1]),
+        "pooled_bit_exact": pooled_equal,
+        "block_decisions": int(decided.sum()),
+        "block_mismatches_outside_band": int((sel[decided] != dev_sel[decided]).sum()),
+        "padded_lists_bit_exact": bool(lists_equal),
+        "rows": seq,
+        "max_abs": float(diff.max()),
+        "mean_abs": float(diff.mean()),
+    }
+    parity["pass"] = (pooled_equal and lists_equal
+                      and parity["block_mismatches_outside_band"] == 0
+                      and parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3)
+    res = {
+        "seq": seq,
+        "workload": "BASELINE config 1: the whole 8k layer (Hq 32, Hkv 8, D 128, alpha 0.1)",
+        "cores": workers,
+        "pool_s": t1 - t0,
+        "selection_s": t2 - t1,
+        "attention_s": t3 - t2,
+        "layer_s": t3 - t0,
+        "retained_flops": flops,
+        "tflops": flops / (t3 - t0) / 1e12,
+        "parity": parity,
+    }
+    log(f"cpu baseline, config 1 (8k, whole layer): {json.dumps(res)}")
+    return res
+
+
+def run_chunked(torch, total: int, chunk: int, alpha: float, *, planted: float = 3.0):
     """one layer's chunked prefill of ``total`` tokens in
     ``chunk``-token query chunks against a growing bf16 KV cache, dense tail
-    only on the last chunk (``total_tokens`` known).  Times the incremental
-    pooled cache (``fpv2.ChunkedPrefill``) and, beside it, the reference
-    hook's per-chunk re-pooling of the whole prefix (``fpv2_sdpa``)."""
+    only on the last chunk (``total_tokens`` known), ``min_tokens = chunk``
+    (so chunk 0 is selected too; the hook's default 4096 would send it to
+    exact attention).  Times the incremental pooled cache
+    (``fpv2.ChunkedPrefill``) and, beside it, the reference hook's per-chunk
+    re-pooling of the whole prefix (``fpv2_sdpa``)."""
     from fpv2 import ChunkedPrefill, FPV2Config
     from fpv2.patch import _fpv2_sdpa
     from fpv2.synthetic import baseline_qkv
 
     dev = torch.device("cuda:0")
-    log(f"chunked {total} in {chunk}-token chunks: generating inputs")
-    q, k, v = baseline_qkv(total, planted=3.0, heavy_fraction=heavy_fraction(total), seed=0,
+    log(f"chunked {total} in {chunk}-token chunks: generating inputs (planted {planted:.2f})")
+    q, k, v = baseline_qkv(total, planted=planted, heavy_fraction=heavy_fraction(total), seed=0,
                            device=dev)
     config = FPV2Config(alpha=alpha, sink_tokens=BLOCK, mean_correction=True)
     scale = D ** -0.5
     stream = torch.cuda.current_stream(dev)
 
     def one_pass(incremental: bool, keeps=None):
-        cp = ChunkedPrefill(HQ, HKV, D, total, config=config, total_tokens=total, device=dev)
+        cp = ChunkedPrefill(HQ, HKV, D, total, config=config, total_tokens=total,
+                            min_tokens=chunk, device=dev)
         events = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -415,6 +534,8 @@ def run_chunked(torch, total: int, chunk: int, alpha: float):
         "chunk": chunk,
         "chunks": -(-total // chunk),
         "alpha": alpha,
+        "planted": planted,
+        "min_tokens": chunk,
         "ms_total": wall,
         "tok_per_s": total / (wall * 1e-3),
         "stage_ms": stage,
@@ -521,6 +642,25 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
         torch.cuda.empty_cache()
+        # config 4 in the sparse regime: the last chunk's dense tail walks
+        # the whole prefix while the other tiles prune most blocks
+        cc = run_chunked(torch, 65536, 2048, args.alpha, planted=3.0 * math.sqrt(D))
+        cc["label"] = ("supplementary: config 4 on the contrast generator (planted key "
+                       "direction x 3*sqrt(D))")
+        extra["chunked_64k_contrast"] = cc
+        torch.cuda.empty_cache()
+        # the other head dimensions and float16 (the reference's
+        # SUPPORTED_HEAD_DIMS and dtypes) on config 2's layer
+        geos = {}
+        for hd, dt in ((64, torch.bfloat16), (96, torch.bfloat16), (256, torch.bfloat16),
+                       (128, torch.float16)):
+            r, _ = run_config(torch, 32768, args.alpha, x_steps, x_warm, head_dim=hd, dtype=dt)
+            geos[f"d{hd}_{str(dt).replace('torch.', '')}"] = {
+                key: r[key] for key in ("head_dim", "dtype", "ms_per_layer", "stage_ms",
+                                        "density", "retained_tflops_attention",
+                                        "mfma_frac_attention")}
+            torch.cuda.empty_cache()
+        extra["other_geometries_32k"] = geos
         from fpv2.prefill_harness import QWEN3_4B, measure
         log("e2e: random-init Qwen3-4B-architecture prefill, 65536 tokens, 2048-token chunks")
         e2e = measure(QWEN3_4B, tokens=65536, chunk=2048, alpha=args.alpha, device="cuda:0")

@@ -105,6 +105,8 @@ struct AttnArgs {
   int G, Hkv, Nt, Nb, Lq, out_rows, Lk, offset, bk, tq, nchunk;
   float c_scale;  // scale * log2(e)
   float shift;    // log2(block_k)
+  float inv_bk;   // 1 / block_k: the exact-phase weights' factor where the
+                  // correction phase starts in the reference-free pass
   int64_t q_hs, k_hs, v_hs, o_hs, o_rs;
   int64_t pooled_hs;  // elements between KV heads of pk / pv
   int q_rs, k_rs, v_rs;
@@ -233,12 +235,21 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     qpos_abs[rg] = a.offset + pos[rg];
   }
 
+  // bfloat16 (8 exponent bits, like float32) takes the reference-free first
+  // pass: Q is loaded pre-multiplied by c = scale*log2(e) (one rounding to
+  // bf16 per element, at most 2^-9 relative), so S = K.Q'^T is already in
+  // log2 units and P = exp2(S) needs no VALU before the exp; rows whose sums
+  // or outputs leave the float32 range walk again with an online reference.
+  // float16 P (5 exponent bits) needs a reference: its first pass takes
+  // each row's max over its first slice and P = exp2(s*c - m_ref).
+  constexpr bool kFree = std::is_same<T, bf16_t>::value;
   vec8 qf[RG][KSQ];
   {
     const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
-    // The softmax folds the scale into one FMA per logit and needs a positive
-    // factor: for scale < 0 the queries are negated instead (s*c = (-s)*(-c)).
-    const uint32_t sign = a.c_scale < 0.f ? 0x80008000u : 0u;
+    // float16: the softmax folds the scale into one FMA per logit and needs
+    // a positive factor: for scale < 0 the queries are negated instead
+    // (s*c = (-s)*(-c)).
+    const uint32_t sign = (!kFree && a.c_scale < 0.f) ? 0x80008000u : 0u;
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
       const uint32_t qoff =
@@ -248,12 +259,20 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
 #pragma unroll
       for (int k = 0; k < KSQ; ++k) {
         u32x4 v = buf_load16(qr, qoff + (row_valid[rg] ? (dhalf * KSQ + k) * 32 : 0));
-        v ^= sign;
+        if constexpr (kFree) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = pack2<T>(__uint_as_float(v[e] << 16) * a.c_scale,
+                            __uint_as_float(v[e] & 0xffff0000u) * a.c_scale);
+        } else {
+          v ^= sign;
+        }
         qf[rg][k] = as_vec8<T>(v);
       }
     }
   }
-  const float c_pos = fmaxf(fabsf(a.c_scale), 1e-30f);
+  // factor from S to log2 units (1 when Q carries it)
+  const float c_pos = kFree ? 1.f : fmaxf(fabsf(a.c_scale), 1e-30f);
 
   // ---- block lists of (h, t), clipped as kernel.py:555-558 ----
   // The counts and the first 64 entries of both lists are requested together
@@ -339,11 +358,14 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // the first 64 entries)
   window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
   int win_next = CORR ? load_window(64) : 0;
-  int walk_it = 0;
+  // A walk covers steps [walk_it, walk_end): all of them, or (the
+  // reference-free pass with correction) the exact steps, then the
+  // correction steps.
+  int walk_it = 0, walk_end = n_steps;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
     const int it = walk_it++;
-    if (it < n_sel) {
+    if (it < n_sel && it < walk_end) {
       if (it - win_base >= 64) {
         win_base += 64;
         if constexpr (CORR) {
@@ -356,7 +378,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
       s.key0 = __builtin_amdgcn_readlane(win_key0, it - win_base);
       s.nkeys = __builtin_amdgcn_readlane(win_nk, it - win_base);
-    } else if (it < n_steps) {
+    } else if (it < walk_end) {
       s.corr = 1;
       s.li = (it - n_sel) * BN;
       s.nkeys = min(pr_count - s.li, BN);
@@ -630,6 +652,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     constexpr bool MASK = decltype(mask_c)::value;
     constexpr int MODE = decltype(mode_c)::value;
     constexpr bool MAX = HN && MODE != 0;
+    // the reference-free first pass: P = exp2(S) (the correction slices'
+    // shift is applied once, as a rescale between the exact and the
+    // correction walks)
+    constexpr bool RAW = kFree && MODE == 0;
     f32x16(&s_new)[RG] = s_buf[B];
     f32x16(&s_old)[RG] = s_buf[1 - B];
     constexpr int KW = KSQ < 4 ? KSQ : 4;  // K fragment reads in flight
@@ -669,7 +695,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       bias[rg] = 0.f;
       // (the logit shift of correction slices selected as scalar bits, so
       // the add takes it from an SGPR)
-      if constexpr (HP)
+      if constexpr (HP && !RAW)
         bias[rg] = bias_of_ref(rg) +
                    __uint_as_float(__builtin_amdgcn_readfirstlane(p_pend.corr ? __float_as_uint(a.shift) : 0u));
     }
@@ -679,8 +705,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     auto exp_pair = [&](auto fc) {
       constexpr int f = decltype(fc)::value;
       constexpr int rg = f % RG, pi = f / RG;
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s_old[rg][2 * pi], c_pos, bias[rg]));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s_old[rg][2 * pi + 1], c_pos, bias[rg]));
+      const float x0 = RAW ? s_old[rg][2 * pi] : fmaf(s_old[rg][2 * pi], c_pos, bias[rg]);
+      const float x1 = RAW ? s_old[rg][2 * pi + 1] : fmaf(s_old[rg][2 * pi + 1], c_pos, bias[rg]);
+      const float p0 = __builtin_amdgcn_exp2f(x0);
+      const float p1 = __builtin_amdgcn_exp2f(x1);
       const uint32_t word = pack2<T>(p0, p1);
       l_run[rg] = add_pair<T>(word, l_run[rg]);  // row sum of the rounded P used below
       w[rg][pi / 4][pi % 4] = word;
@@ -884,8 +912,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   using P1 = std::integral_constant<int, 1>;
   auto run_walk = [&](auto online_c) {
     constexpr bool ONLINE = decltype(online_c)::value;
-    using MFirst = std::integral_constant<int, ONLINE ? 2 : 1>;
+    // (the reference-free pass computes no row max, not even for the first slice)
+    using MFirst = std::integral_constant<int, ONLINE ? 2 : (kFree ? 0 : 1)>;
     using MRest = std::integral_constant<int, ONLINE ? 2 : 0>;
+    const int count = walk_end - walk_it;  // sub-tiles of this walk
     Step pend[LA];
 #pragma unroll
     for (int p = 0; p < LA; ++p) {
@@ -911,15 +941,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       else process(True{}, True{}, NewB{}, MRest{}, s0);
       cstage = cstage == NST - 1 ? 0 : cstage + 1;
     };
-    if (n_steps > 0) {
+    if (count > 0) {
       do_step(True{}, P0{});  // the first sub-tile has no pending slice
       // the pending buffer alternates, so two sub-tiles per iteration
       int it = 1;
-      for (; it + 1 < n_steps; it += 2) {
+      for (; it + 1 < count; it += 2) {
         do_step(False{}, P1{});
         do_step(False{}, P0{});
       }
-      if (it < n_steps) {
+      if (it < count) {
         do_step(False{}, P1{});
         process(False{}, True{}, P1{}, MRest{}, p_pend);  // pending in s_buf[0]
       } else {
@@ -930,12 +960,16 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     vm_wait<0>();
   };
 
-  // First pass: each row's reference is the max of its first slice and is
-  // never updated, so the walk computes no row max and never rescales O.
-  // P = exp2(s*c - m_ref) may then exceed 1 by any factor: float32 sums and
-  // bfloat16 P hold it unless the range is exceeded.  A valid row whose sum
-  // leaves [2^-60, 2^100] (or is NaN) sends the workgroup through the walk
-  // again with the online reference and rescale (kernel.py:287-310).
+  // First pass: no row's reference is ever updated, so the walk computes no
+  // row max and never rescales O.  bfloat16: P = exp2(S) with no reference
+  // (the logits in log2 units); float16: the reference is the max of the
+  // row's first slice, P = exp2(s*c - m_ref).  P may then exceed 1 by any
+  // factor: float32 sums and the 8-bit exponent of bfloat16 P hold it unless
+  // the range is exceeded (float16 P past 2^16 is inf).  A valid row whose
+  // sum leaves [2^-60, 2^64], or whose O holds an inf or NaN, sends the
+  // workgroup through the walk again with the online reference and rescale
+  // (kernel.py:287-310), where P <= 2^8.  The bound 2^64 keeps O finite for
+  // |V| up to about 2^64; the finiteness test covers larger V.
   // DS = 2: row sums over all keys, the two waves' sums of their own keys
   // added in either order, so both waves hold the same value.
   float l_pair = 0.f;
@@ -948,13 +982,41 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     }
   };
   auto row_sum = [&](int rg) { return KSPLIT ? l_pair : pair_sum(l_run[rg]); };
-  run_walk(False{});
+  if constexpr (kFree && CORR) {
+    // exact steps, then the correction steps: in between, every weight so
+    // far is scaled by 2^-shift = 1/block_k, which gives the pooled entries,
+    // taken as exp2(S), their relative weight 2^shift (kernel.py:349-351);
+    // O / l is unchanged by the common factor.  (A rescale inside the walk
+    // would make the compiler move O between register ranges every slice.)
+    walk_end = n_sel;
+    run_walk(False{});
+    if (n_corr > 0) {
+      __syncthreads();  // every wave is done with the ring before it is refilled
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        l_run[rg] *= a.inv_bk;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) scale_in_place(o[rg][dt], a.inv_bk);
+      }
+      walk_it = n_sel;
+      walk_end = n_steps;
+      run_walk(False{});
+    }
+  } else {
+    run_walk(False{});
+  }
   pair_row_sum();
   bool bad = false;
 #pragma unroll
   for (int rg = 0; rg < RG; ++rg) {
     const float l = row_sum(rg);
-    bad = bad || (row_valid[rg] && !(l >= 0x1p-60f && l <= 0x1p100f));
+    bool fin = true;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) fin = fin && __builtin_isfinite(o[rg][dt][j]);
+    }
+    bad = bad || (row_valid[rg] && !(l >= 0x1p-60f && l <= 0x1p64f && fin));
   }
   // Workgroup-wide decision through the last ring stage, which the second
   // walk refills only after its first barrier (the flags are read by then).
@@ -978,6 +1040,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     }
     p_pend = Slice{0, 0, 0, 0u};
     walk_it = 0;
+    walk_end = n_steps;
     win_base = 0;
     window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
     if constexpr (CORR) win_next = load_window(64);
@@ -1127,6 +1190,7 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
   a.tq = static_cast<int>(p->tile_q);
   a.c_scale = static_cast<float>(p->scale * 1.4426950408889634);
   a.shift = static_cast<float>(__builtin_log2(static_cast<double>(p->block_k)));
+  a.inv_bk = static_cast<float>(1.0 / static_cast<double>(p->block_k));
   a.q_hs = p->q_head_stride;
   a.k_hs = p->k_head_stride;
   a.v_hs = p->v_head_stride;

@@ -22,12 +22,20 @@ applies only once the cache reaches it (``patch.py:55-63``); below
 ``min_tokens`` keys, or with fewer queries than one selection tile, the hook
 hands the call to the original attention (``patch.py:177-205``), and here the
 same kernels run exact causal attention instead (``alpha = 0`` selects every
-visible block, and with no pruned block the correction is empty).
+visible block, and with no pruned block the correction is empty).  A prefix
+longer than the selection kernel holds (more than ``FPV2_MAX_BLOCKS`` key
+blocks), which the hook also hands to the original attention, runs exact
+causal attention too: the attention kernel walks every visible block of
+lists built without the selection kernel.
 
 With ``collect_stats`` the layer counts selected and visible blocks as the
 hook's ``block_sparsity`` does (``patch.py:66-88``): selected counts are kept
 on the device and summed in batches (``SelectedBlockCounter``), and
-``block_sparsity()`` synchronises once to read them.
+``block_sparsity()`` synchronises once to read them.  Exact calls count as
+dense, and a chunk of fewer queries than one tile is not counted, as the
+hook's accounting rule leaves such calls out (``patch.py:255-266``).  These
+counts are the layer's own: the calls do not enter the hook's
+``fpv2.block_sparsity()``.
 
 Every call runs on the current stream.  As with a module's buffers, the KV
 and pooled caches are not synchronised across streams: a caller that moves
@@ -41,7 +49,7 @@ from dataclasses import replace
 import torch
 
 from fpv2 import _lib
-from fpv2.kernel import SUPPORTED_HEAD_DIMS
+from fpv2.kernel import SUPPORTED_HEAD_DIMS, _launch_attention
 from fpv2.patch import (SelectedBlockCounter, _causal_block_count, _effective_config, _geometry,
                         _pool_into, _request_config, _select_attend)
 from fpv2.selection import FPV2Config
@@ -203,7 +211,8 @@ class ChunkedPrefill:
         device = _lib.require_device(q3, self.k)
         lib = _lib.load()
         k3, v3 = self.k[:, :self.length], self.v[:, :self.length]
-        geo = _geometry(q3[None], k3[None], v3[None], self.request_config(q3.shape[1]))
+        geo = _geometry(q3[None], k3[None], v3[None], self.request_config(q3.shape[1]),
+                        capped=False)
         with torch.cuda.device(device):
             if marks is not None:
                 marks("pool")
@@ -221,14 +230,49 @@ class ChunkedPrefill:
         call_scale = self.head_dim ** -0.5 if scale is None else scale
         if self.collect_stats and keep is None:
             keep = {}
-        _select_attend(q3, k3, v3, self.pooled_k[:, :geo.num_blocks],
-                       self.pooled_v[:, :geo.num_blocks], geo, scale=call_scale, out=out,
-                       marks=marks, keep=keep)
-        if self.collect_stats:
+        pooled_k = self.pooled_k[:, :geo.num_blocks]
+        pooled_v = self.pooled_v[:, :geo.num_blocks]
+        if geo.num_blocks <= _lib.MAX_BLOCKS:
+            _select_attend(q3, k3, v3, pooled_k, pooled_v, geo, scale=call_scale, out=out,
+                           marks=marks, keep=keep, hook_stats=False)
+        else:
+            self._exact_attend(q3, k3, v3, pooled_k, pooled_v, geo, scale=call_scale,
+                               out=out, marks=marks, keep=keep)
+        if self.collect_stats and geo.query_length >= geo.config.tile_q:
             self._selected.add(keep["lists"][1])
             self._visible += _causal_block_count(self.kv_heads, geo.query_length, geo.offset,
                                                  geo.config)
         return out[None]
+
+    @staticmethod
+    def _exact_attend(q3, k3, v3, pooled_k, pooled_v, geo, *, scale, out, marks, keep):
+        """Exact causal attention for a prefix past the selection kernel's
+        block limit: the lists the selection would give at ``alpha = 0``
+        (every block that starts at or before the tile's last row, in
+        ascending order; nothing pruned), built here, then the attention
+        kernel."""
+        config, device = geo.config, q3.device
+        hkv, nt, nb = geo.kv_heads, geo.num_tiles, geo.num_blocks
+        if marks is not None:
+            marks("select")
+        ids = torch.arange(nb, dtype=torch.int32, device=device).expand(hkv, nt, nb).contiguous()
+        tiles = torch.arange(nt, dtype=torch.int64, device=device)
+        tile_last = geo.offset + torch.clamp((tiles + 1) * config.tile_q, max=geo.query_length) - 1
+        counts = torch.clamp(tile_last // config.block_k + 1, max=nb).to(torch.int32)
+        counts = counts.expand(hkv, nt).contiguous()
+        pruned_counts = torch.zeros_like(counts)
+        if marks is not None:
+            marks("attention")
+        _launch_attention(
+            q3, k3, v3, pooled_k, pooled_v, ids, counts, ids, pruned_counts, out,
+            device=device, scale=scale, config=config, offset=geo.offset,
+            query_length=geo.query_length, key_length=geo.key_length, num_blocks=nb,
+            padded_query_length=geo.padded_query_length, out_rows=geo.query_length)
+        if marks is not None:
+            marks("done")
+        if keep is not None:
+            keep.update(config=config, offset=geo.offset, pooled_k=pooled_k, pooled_v=pooled_v,
+                        lists=(ids, counts, ids, pruned_counts))
 
     def step(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, **kwargs) -> torch.Tensor:
         """Append the chunk's K/V, then attend its queries."""

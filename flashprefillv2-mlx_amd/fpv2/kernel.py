@@ -29,12 +29,14 @@ SUPPORTED_HEAD_DIMS = (64, 96, 128, 256)
 
 @dataclass(frozen=True)
 class TileConfig:
-    """Tile dimensions of the reference's Metal kernel (``kernel.py:30-57``).
+    """A tile request: ``bq`` query rows, ``bk`` keys, ``wm`` warps
+    (the names of ``kernel.py:30-40``).
 
-    Kept for interface parity: ``sparse_attention`` validates a given tile
-    with the reference's rules, and the PackGQA alignment rule uses ``bq``.
-    The gfx950 kernel's own tiling (128 packed rows x 32-key sub-tiles; 4
-    waves, 8 for head_dim 256) is fixed per head dimension.
+    The gfx950 kernel's tiling is fixed per head dimension (128 packed query
+    rows per workgroup, 32-key sub-tiles, 4 waves; 8 for head_dim 256), so a
+    tile changes neither the launch nor the output.  ``sparse_attention``
+    accepts one for interface parity, checks that it is well formed, and
+    uses its ``bq`` in the PackGQA alignment rule (``kernel.py:505-510``).
     """
 
     bq: int
@@ -46,21 +48,15 @@ class TileConfig:
         return 32 * self.wm
 
     def check(self, head_dim: int, *, block_k: int = 128, tile_q: int = 128) -> None:
-        if min(self.bq, self.bk, self.wm) <= 0:
+        """Well-formedness only: positive integer dimensions and a head
+        dimension the kernel is built for.  (The reference's threadgroup
+        memory and simdgroup fragment rules describe Apple GPUs and do not
+        apply to this kernel.)"""
+        dims = (self.bq, self.bk, self.wm)
+        if any(isinstance(x, bool) or not isinstance(x, int) or x <= 0 for x in dims):
             raise ValueError("tile dimensions must be positive")
-        if self.bq % (8 * self.wm):
-            raise ValueError("bq must contain whole 8-row fragments per simdgroup")
-        if block_k % self.bk:
-            raise ValueError("bk must divide block_k")
-        if tile_q < self.bq or tile_q % self.bq:
-            raise ValueError("bq must divide tile_q")
-        if (self.bk * head_dim) % self.threads:
-            raise ValueError("thread count must divide the correction gather")
-        memory = (self.bq * (head_dim + 8) + max(
-            head_dim * (self.bk + 8), self.bk * (head_dim + 8)
-        )) * 2
-        if memory > 32 * 1024:
-            raise ValueError("tile exceeds 32 KB of threadgroup memory")
+        if head_dim not in SUPPORTED_HEAD_DIMS:
+            raise ValueError(f"head dimension must be one of {SUPPORTED_HEAD_DIMS}")
 
 
 _DEFAULT_TILES = {
@@ -80,7 +76,11 @@ def default_tile(head_dim: int) -> TileConfig:
 
 
 def _tile_for_config(head_dim: int, config: FPV2Config) -> TileConfig:
-    """Tile resolution of the reference (``kernel.py:76-88``)."""
+    """The tile named for a configuration (``kernel.py:76-88``): the
+    head-dimension default when it divides ``tile_q`` and ``block_k``,
+    otherwise ``(min(tile_q, 32), min(block_k, 16), bq / 8)`` (at least one
+    warp).  Any positive ``tile_q`` and ``block_k`` resolve: the kernel
+    takes them all."""
     tile = default_tile(head_dim)
     if (
         config.tile_q >= tile.bq
@@ -88,11 +88,9 @@ def _tile_for_config(head_dim: int, config: FPV2Config) -> TileConfig:
         and config.block_k % tile.bk == 0
     ):
         return tile
-    if config.tile_q % 8 or config.block_k % 8:
-        raise ValueError("block_k and tile_q must be multiples of 8 for Steel")
     bq = min(config.tile_q, 32)
     bk = min(config.block_k, 16)
-    return TileConfig(bq, bk, bq // 8)
+    return TileConfig(bq, bk, max(1, bq // 8))
 
 
 def compact_block_indices(

@@ -16,9 +16,13 @@ top-left and bottom-right diagonals coincide), or ``attn_mask`` a
 in torch and therefore passed through.
 
 For eligible calls ``offset = key_length - query_length`` places the query
-chunk in the causal key prefix.  Nothing is padded or copied: the kernels take
-head/row strides and valid lengths, treat rows past them as zeros, and write
-the ``[1, Hq, Lq, D]`` output directly.  ``disable`` restores the original.
+chunk in the causal key prefix.  An eligible call whose key range needs more
+blocks than the selection kernel holds (``FPV2_MAX_BLOCKS``, 1 048 576 keys
+at ``block_k`` 128) goes to the original function too, and counts as dense
+in ``block_sparsity`` as a call below ``min_tokens`` does.  Nothing is padded
+or copied: the kernels take head/row strides and valid lengths, treat rows
+past them as zeros, and write the ``[1, Hq, Lq, D]`` output directly.
+``disable`` restores the original.
 """
 
 from __future__ import annotations
@@ -41,6 +45,7 @@ except ImportError:  # pragma: no cover - older torch
 _ORIGINAL_SDPA = F.scaled_dot_product_attention
 _enabled = False
 _collect_stats = False
+_forwarding = False  # inside a pass-through's CausalBias dispatch
 
 
 class SelectedBlockCounter:
@@ -77,10 +82,13 @@ class SelectedBlockCounter:
             for stream in self._streams:
                 if stream != current:
                     current.wait_stream(stream)
-            # the allocator must not reuse a kept tensor's memory on its own
-            # stream before this stream has read it
+            # the allocator must not reuse a kept tensor's memory, nor the
+            # previous total's (allocated on an earlier fold's stream), on its
+            # own stream before this stream has read it
             for c in self._pending:
                 c.record_stream(current)
+            if self._total is not None and self._total.is_cuda:
+                self._total.record_stream(current)
         part = torch.cat([c.reshape(-1) for c in self._pending]).sum(dtype=torch.int64)
         self._total = part if self._total is None else self._total + part
         self._pending.clear()
@@ -156,14 +164,17 @@ def block_sparsity() -> float:
     return 1.0 - selected / _visible_blocks
 
 
-def _pad_sequence(x: torch.Tensor, length: int) -> torch.Tensor:
-    """Zero-pad the sequence (penultimate) axis to ``length``."""
-    amount = length - x.shape[-2]
-    if amount < 0:
-        raise ValueError("target length cannot be shorter than the input")
-    if not amount:
-        return x
-    return F.pad(x, (0, 0, 0, amount))
+def _num_blocks(query_length: int, key_length: int, config: FPV2Config) -> int:
+    """Key blocks of a call: ``ceil(max(Lk, offset + Lq_pad) / block_k)``
+    (``patch.py:123-131``)."""
+    padded_query_length = -(-query_length // config.tile_q) * config.tile_q
+    required = max(key_length, key_length - query_length + padded_query_length)
+    return -(-required // config.block_k)
+
+
+def _within_block_limit(query_length: int, key_length: int, config: FPV2Config) -> bool:
+    """Whether the selection kernel holds the call's key blocks."""
+    return _num_blocks(query_length, key_length, config) <= _lib.MAX_BLOCKS
 
 
 def fpv2_sdpa(
@@ -199,10 +210,11 @@ class _Geometry:
     num_blocks: int
 
 
-def _geometry(q, k, v, config: FPV2Config) -> _Geometry:
+def _geometry(q, k, v, config: FPV2Config, *, capped: bool = True) -> _Geometry:
     """The reference hook's validation (``patch.py:102-124``) and the block
     grid: Q padded to a ``tile_q`` multiple, keys to ``ceil(max(Lk, off +
-    Lq_pad) / block_k)`` blocks, as index arithmetic only."""
+    Lq_pad) / block_k)`` blocks, as index arithmetic only.  ``capped``:
+    refuse more blocks than the selection kernel holds."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("q, k, and v must have shape [batch, heads, sequence, dim]")
     if q.shape[0] != 1 or k.shape[0] != 1 or v.shape[0] != 1:
@@ -223,10 +235,8 @@ def _geometry(q, k, v, config: FPV2Config) -> _Geometry:
         raise ValueError("q, k, and v must share float16 or bfloat16 dtype")
     offset = key_length - query_length
     padded_query_length = -(-query_length // config.tile_q) * config.tile_q
-    required_key_length = max(key_length, offset + padded_query_length)
-    padded_key_length = -(-required_key_length // config.block_k) * config.block_k
-    num_blocks = padded_key_length // config.block_k
-    if num_blocks > _lib.MAX_BLOCKS:
+    num_blocks = _num_blocks(query_length, key_length, config)
+    if capped and num_blocks > _lib.MAX_BLOCKS:
         raise ValueError(f"key length needs {num_blocks} blocks; at most {_lib.MAX_BLOCKS}")
     return _Geometry(config=config, query_heads=q.shape[1], kv_heads=k.shape[1],
                      head_dim=q.shape[-1], query_length=query_length, key_length=key_length,
@@ -255,10 +265,13 @@ def _pool_into(lib, k3, v3, pooled_k, pooled_v, *, dtype, valid_rows, num_blocks
 
 
 def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out=None,
-                   marks=None, keep=None):
+                   marks=None, keep=None, hook_stats=True):
     """Selection and block-sparse attention of one hook call, given the
     pooled K/V (``[Hkv, >=Nb, D]`` views sharing one head stride).  Writes
-    ``out`` (``[Hq, Lq, D]``, allocated when None) and returns it."""
+    ``out`` (``[Hq, Lq, D]``, allocated when None) and returns it.
+    ``hook_stats``: count the call in the hook's ``block_sparsity`` while
+    statistics are on (``patch.py:150-155``); callers with counters of
+    their own pass False."""
     config = geo.config
     device = q3.device
     lib = _lib.load()
@@ -282,7 +295,7 @@ def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out
             q3.data_ptr(), pooled_k.data_ptr(), dtype, params, None, None, ids.data_ptr(),
             counts.data_ptr(), pruned_ids.data_ptr(), pruned_counts.data_ptr(), stream)
         _lib.check(status, "score_select")
-    if _collect_stats:
+    if _collect_stats and hook_stats:
         global _visible_blocks
         total = _selected_totals.get(counts.device)
         if total is None:
@@ -378,6 +391,30 @@ def _eligible(q, k, v, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
     return _bottom_right_causal(q, k, attn_mask, is_causal)
 
 
+def _call_original(query, key, value, attn_mask, dropout_p, is_causal, scale, enable_gqa,
+                   kwargs):
+    """The original function on a passed-through call's arguments.
+
+    torch routes a ``CausalBias`` mask through the bias's own dispatch only
+    while ``F.scaled_dot_product_attention`` is the original function
+    (``CausalBias.__torch_function__``); with the hook installed that test
+    fails and the bias would reach the kernel as a plain tensor.  Such calls
+    therefore take the bias's dispatch here, as the original would; the
+    calls it makes back into ``F.scaled_dot_product_attention`` (a square
+    causal call, or the materialised mask) go straight to the original."""
+    global _forwarding
+    if (CausalBias is not None and isinstance(attn_mask, CausalBias) and not kwargs
+            and not _forwarding):
+        _forwarding = True
+        try:
+            return CausalBias._dispatch(query, key, value, attn_mask, dropout_p=dropout_p,
+                                        is_causal=is_causal, scale=scale, enable_gqa=enable_gqa)
+        finally:
+            _forwarding = False
+    return _ORIGINAL_SDPA(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                          is_causal=is_causal, scale=scale, enable_gqa=enable_gqa, **kwargs)
+
+
 def enable(
     config: FPV2Config | None = None,
     *,
@@ -409,6 +446,10 @@ def enable(
 
     def wrapped(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
                 scale=None, enable_gqa=False, **kwargs):
+        if _forwarding:  # a call made by a pass-through's CausalBias dispatch
+            return _ORIGINAL_SDPA(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                                  is_causal=is_causal, scale=scale, enable_gqa=enable_gqa,
+                                  **kwargs)
         four_d = all(isinstance(t, torch.Tensor) and t.ndim == 4 for t in (query, key))
         call_config = _effective_config(config, query.shape[1], key.shape[1]) if four_d else None
         if call_config is not None:
@@ -416,9 +457,10 @@ def enable(
         if call_config is not None and _eligible(
             query, key, value, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
             call_config, min_tokens
-        ):
+        ) and _within_block_limit(query.shape[-2], key.shape[-2], call_config):
             call_scale = query.shape[-1] ** -0.5 if scale is None else scale
             return fpv2_sdpa(query, key, value, scale=call_scale, config=call_config)
+        # dense calls: below min_tokens, or more key blocks than selection holds
         if _collect_stats and call_config is not None and _eligible(
             query, key, value, attn_mask, dropout_p, is_causal, enable_gqa, kwargs,
             call_config, 1
@@ -429,9 +471,8 @@ def enable(
             )
             _selected_dense_blocks += visible
             _visible_blocks += visible
-        return _ORIGINAL_SDPA(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
-                              is_causal=is_causal, scale=scale, enable_gqa=enable_gqa,
-                              **kwargs)
+        return _call_original(query, key, value, attn_mask, dropout_p, is_causal, scale,
+                              enable_gqa, kwargs)
 
     F.scaled_dot_product_attention = wrapped
     _enabled = True

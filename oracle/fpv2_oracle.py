@@ -521,21 +521,92 @@ def fpv2_sdpa_oracle(q, k, v, *, scale: float, config=OracleConfig(),
 
 
 # --------------------------------------------------------------------------
-# Work accounting (retained FLOPs) for measurements
+# Whole calls over tile ranges (parallel threads)
 # --------------------------------------------------------------------------
 
-def visible_key_counts(num_tiles, num_blocks, *, tile_q, block_k, offset,
-                       query_length, key_length) -> np.ndarray:
-    """``[Nt, Nb]``: sum over the tile's valid rows of causally visible keys
-    in each block — the per-block work of the exact phase."""
-    out = np.zeros((num_tiles, num_blocks), dtype=np.int64)
-    bstart = np.arange(num_blocks) * block_k
-    bend = np.minimum(bstart + block_k, key_length)
-    for t in range(num_tiles):
-        rows = np.arange(t * tile_q, min((t + 1) * tile_q, query_length))
-        if rows.size == 0:
-            continue
-        lim = np.minimum(offset + rows + 1, key_length)  # keys < lim visible
-        vis = np.clip(np.minimum(lim[:, None], bend[None, :]) - bstart[None, :], 0, None)
-        out[t] = vis.sum(axis=0)
+def _tile_ranges(num_tiles, tile_q, offset, parts, last_n):
+    """Contiguous tile ranges of about equal causal work (a tile's keys grow
+    with its position); the last range keeps at least ``last_n`` tiles, so
+    the dense tail is decided within one range."""
+    work = offset + (np.arange(num_tiles) + 1) * tile_q
+    cum = np.cumsum(work)
+    bounds = np.searchsorted(cum, cum[-1] * np.arange(1, parts) / parts, side="left") + 1
+    edges = sorted({0, num_tiles, *[int(b) for b in bounds if 0 < b < num_tiles]})
+    ranges = [[a, b] for a, b in zip(edges[:-1], edges[1:])]
+    if len(ranges) > 1 and ranges[-1][1] - ranges[-1][0] < last_n:
+        last = ranges.pop()
+        ranges[-1][1] = last[1]
+    return ranges
+
+
+def _map_ranges(fn, ranges, workers):
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+    if workers <= 1:
+        return [fn(r) for r in ranges]
+    # numpy releases the GIL in its ufuncs and BLAS calls; BLAS runs
+    # single-threaded per range (the limit is process-wide: set once)
+    with threadpool_limits(limits=1), ThreadPoolExecutor(max_workers=workers) as pool:
+        return list(pool.map(fn, ranges))
+
+
+def select_tile_ranges(q, pooled_k, *, scale, config=OracleConfig(), offset: int = 0,
+                       query_length: int | None = None, workers: int = 1,
+                       chunk_tiles: int = 32):
+    """``block_scores_and_select`` of a whole call, evaluated as calls of
+    contiguous tile ranges (each at its own offset, the dense tail kept only
+    in the range that ends the call) on ``workers`` threads.  Tiles are
+    independent (selection.py:144-201 scores them in any grouping), so the
+    result equals the one-call selection.  Returns ``(selected, ratio)``."""
+    q = np.asarray(q)
+    tq = config.tile_q
+    lq_pad = q.shape[1]
+    valid = lq_pad if query_length is None else query_length
+    nt = lq_pad // tq  # (every tile holds a valid row: lq_pad = ceil(valid / tq) * tq)
+    ranges = _tile_ranges(nt, tq, offset, max(1, 4 * workers), config.last_n_blocks)
+
+    def one(r):
+        t0, t1 = r
+        sub = config if t1 == nt else _replace(config, last_n_blocks=0)
+        rows0, rows1 = t0 * tq, t1 * tq
+        sel, _, ratio = block_scores_and_select(
+            q[:, rows0:rows1], pooled_k, scale=scale,
+            config=_replace(sub, score_chunk_tiles=chunk_tiles), offset=offset + rows0,
+            query_length=min(rows1, valid) - rows0, return_ratio=True)
+        return sel, ratio
+
+    parts = _map_ranges(one, ranges, workers)
+    return (np.concatenate([p[0] for p in parts], axis=1),
+            np.concatenate([p[1] for p in parts], axis=1))
+
+
+def attention_tile_ranges(q, k, v, *, scale: float, selected, pooled_k, pooled_v,
+                          config=OracleConfig(), offset: int = 0,
+                          query_length: int | None = None, key_length: int | None = None,
+                          workers: int = 1, dtype=np.float32, row_block: int = 256):
+    """``fpv2_attention_blockwise`` of a whole call, evaluated over
+    contiguous tile ranges on ``workers`` threads.  Rows are independent, so
+    the result equals the one-call evaluation.  Returns ``[Hq, Lq_pad, D]``."""
+    q = np.asarray(q)
+    tq = config.tile_q
+    hq, lq_pad, d = q.shape
+    valid = lq_pad if query_length is None else query_length
+    nt = lq_pad // tq
+    selected = np.asarray(selected, dtype=bool)
+    out = np.zeros((hq, lq_pad, d), dtype=dtype)
+    ranges = _tile_ranges(nt, tq, offset, max(1, 4 * workers), 0)
+
+    def one(r):
+        t0, t1 = r
+        rows0, rows1 = t0 * tq, t1 * tq
+        if rows0 >= valid:
+            return
+        out[:, rows0:rows1] = fpv2_attention_blockwise(
+            q[:, rows0:rows1], k, v, scale=scale, selected=selected[:, t0:t1],
+            pooled_k=pooled_k, pooled_v=pooled_v, config=config, offset=offset + rows0,
+            query_length=min(rows1, valid) - rows0, key_length=key_length, dtype=dtype,
+            row_block=row_block)
+
+    _map_ranges(one, ranges, workers)
     return out

@@ -51,3 +51,15 @@ def attention_errors(actual, expected, valid=None) -> dict:
         "mean_abs": float(diff.mean()),
         "rel": float(diff.max() / max(np.abs(e).max(), 1e-8)),
     }
+
+
+def oracle_select_parallel(q, pooled_k, *, scale, config, offset=0, query_length=None):
+    """The oracle's selection of a whole call on the host's cores (at most 16
+    threads), over tile ranges.  Returns ``(selected, ratio)``."""
+    import os
+
+    from oracle import fpv2_oracle as orc
+
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    return orc.select_tile_ranges(q, pooled_k, scale=scale, config=config, offset=offset,
+                                  query_length=query_length, workers=workers)

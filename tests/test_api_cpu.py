@@ -142,8 +142,24 @@ def test_default_tile_dispatch():
 def test_tile_fallback_for_hook_tile():
     # The hook's 32-position tile falls back to (32, 16, 4) (kernel.py:76-88).
     assert _tile_for_config(128, FPV2Config(tile_q=32)) == TileConfig(32, 16, 4)
-    with pytest.raises(ValueError, match="32 KB"):
-        TileConfig(64, 64, 8).check(256, block_k=128, tile_q=128)
+    # tiles of fewer than 8 positions (GQA groups of 32) resolve too: the
+    # gfx950 kernel takes any tile_q
+    assert _tile_for_config(128, FPV2Config(tile_q=4)) == TileConfig(4, 16, 1)
+    assert _tile_for_config(64, FPV2Config(tile_q=12, block_k=20)) == TileConfig(12, 16, 1)
+
+
+def test_tile_check_is_well_formedness_only():
+    """A tile changes neither the gfx950 launch nor the output: only positive
+    integer dimensions and a supported head dimension are required (the
+    reference's Apple threadgroup-memory rule is not applied)."""
+    TileConfig(64, 64, 8).check(256, block_k=128, tile_q=128)
+    TileConfig(64, 32, 4).check(128, block_k=128, tile_q=32)
+    for bad in (TileConfig(0, 32, 4), TileConfig(32, -1, 4), TileConfig(32, 32, True),
+                TileConfig(32, 32.0, 4)):
+        with pytest.raises(ValueError, match="positive"):
+            bad.check(128)
+    with pytest.raises(ValueError, match="head dimension"):
+        TileConfig(32, 32, 4).check(80)
 
 
 # ---- hook helpers (patch.py:41-63) -----------------------------------------
@@ -333,6 +349,75 @@ def test_score_select_rejects_more_than_the_maximum_block_count():
                                    None, None)
     assert status == _lib.FPV2_ERR_UNSUPPORTED
     assert b"exceeds 8192" in lib.fpv2_last_error()
+
+
+def test_block_count_and_the_selection_limit():
+    """Key blocks of a hook call, ``ceil(max(Lk, offset + Lq_pad) / block_k)``
+    (``patch.py:123-131``), and the hook's routing rule: eligible calls with
+    more blocks than the selection kernel holds go to the original SDPA."""
+    from fpv2.patch import _num_blocks, _within_block_limit
+    cfg = FPV2Config(tile_q=32, block_k=128)
+    assert _num_blocks(32, 128, cfg) == 1
+    assert _num_blocks(33, 129, cfg) == 1 + 1  # Lq_pad 64 -> 96 + 64 = 160 keys
+    assert _num_blocks(1, 100, cfg) == 2       # offset 99 + Lq_pad 32 = 131 keys
+    top = _lib.MAX_BLOCKS * 128
+    assert _num_blocks(32, top, cfg) == _lib.MAX_BLOCKS
+    assert _within_block_limit(32, top, cfg)
+    assert not _within_block_limit(32, top + 1, cfg)
+    # the query padding alone can cross the limit
+    assert not _within_block_limit(20, top - 10, cfg)
+    assert _within_block_limit(20, top - 12, cfg)
+
+
+def test_hook_passes_calls_past_the_block_limit_to_the_original(monkeypatch):
+    """An otherwise eligible call past the block limit reaches the original
+    SDPA and is counted as dense (as a call below ``min_tokens``)."""
+    import fpv2.patch as patch
+    seen = {}
+
+    def fake_original(q, k, v, **kwargs):
+        seen["original"] = True
+        return q
+
+    def fake_fpv2(*args, **kwargs):
+        raise AssertionError("FPV2 path taken past the block limit")
+
+    monkeypatch.setattr(patch, "_ORIGINAL_SDPA", fake_original)
+    monkeypatch.setattr(patch, "fpv2_sdpa", fake_fpv2)
+    monkeypatch.setattr(patch, "_eligible", lambda *a, **k: True)  # device rules aside
+    monkeypatch.setattr(_lib, "MAX_BLOCKS", 4)
+    patch.enable(min_tokens=1, collect_stats=True)
+    q = torch.zeros((1, 4, 32, 64), dtype=torch.bfloat16)
+    kv = torch.zeros((1, 1, 5 * 128, 64), dtype=torch.bfloat16)
+    F.scaled_dot_product_attention(q, kv, kv, is_causal=True, enable_gqa=True)
+    assert seen == {"original": True}
+    assert patch._visible_blocks == patch._selected_dense_blocks == 5
+    assert patch.block_sparsity() == 0.0
+    kv4 = kv[:, :, :4 * 128]
+    with pytest.raises(AssertionError, match="FPV2 path"):
+        F.scaled_dot_product_attention(q, kv4, kv4, is_causal=True, enable_gqa=True)
+
+
+@pytest.mark.parametrize(("lq", "lk", "variant"), [(8, 40, "lower_right"), (24, 24, "lower_right"),
+                                                   (8, 40, "upper_left")])
+def test_passed_through_causal_bias_calls_equal_the_original(lq, lk, variant):
+    """torch dispatches a CausalBias mask only while F.scaled_dot_product_attention
+    is the original function; a call the hook passes through (here: CPU
+    tensors, with GQA) still returns the original's result bit for bit, and
+    the bias's inner calls are not counted twice."""
+    from torch.nn.attention.bias import causal_lower_right, causal_upper_left
+    import fpv2.patch as patch
+    g = torch.Generator().manual_seed(lq + lk)
+    q = torch.randn((1, 4, lq, 16), generator=g)
+    k = torch.randn((1, 2, lk, 16), generator=g)
+    v = torch.randn((1, 2, lk, 16), generator=g)
+    bias = (causal_lower_right if variant == "lower_right" else causal_upper_left)(lq, lk)
+    expected = _ORIGINAL_SDPA(q, k, v, attn_mask=bias, enable_gqa=True)
+    enable(min_tokens=1, collect_stats=True)
+    actual = F.scaled_dot_product_attention(q, k, v, attn_mask=bias, enable_gqa=True)
+    assert torch.equal(actual, expected)
+    assert patch._visible_blocks == 0  # CPU tensors are not eligible at all
+    assert not patch._forwarding
 
 
 def test_kernel_ready_realigns_a_contiguous_view_off_a_16_byte_boundary():

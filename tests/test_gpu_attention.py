@@ -239,6 +239,34 @@ def test_logits_far_above_the_first_slice(cuda, strength, what, head_dim):
     assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
 
 
+@pytest.mark.parametrize("v_scale", [1e9, 1e30])
+@pytest.mark.parametrize("head_dim", [128, 256])
+def test_late_outlier_with_large_values(cuda, v_scale, head_dim):
+    """A late logit outlier (~40 log2 units above the rest of its rows) with
+    |V| around 1e9 or 1e30 in bfloat16.  The first pass keeps every weight
+    below 2^64, so O stays finite for |V| = 1e9 (2^30) and the output is
+    that pass's; at 1e30 (2^100) O overflows float32, which sends the
+    workgroup through the online walk, whose weights are at most 2^8.
+    Compared with exact attention in float64, relative to |V|."""
+    s = 18.5 * (head_dim / 128) ** 0.25
+    q, k, v = _planted_outlier(1024, strength=s, seed=23, d=head_dim)
+    v = v * v_scale
+    config = FPV2Config(alpha=0.0, sink_tokens=0, window_tokens=0, last_n_blocks=0,
+                        mean_correction=False, tile_q=32)
+    scale = head_dim ** -0.5
+    qd, kd, vd = (x.to(torch.bfloat16).to(cuda) for x in (q, k, v))
+    pk, pv = pool_blocks(kd, 128), pool_blocks(vd, 128)
+    selected, _ = block_scores_and_select(qd, pk, scale=scale, config=config)
+    lists = compact_block_indices(selected, config=config, query_length=1024, key_length=1024)
+    out = sparse_attention(qd, kd, vd, pk, pv, *lists, scale=scale, config=config)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float64) / v_scale
+    assert np.isfinite(got).all()
+    exact = orc.exact_causal_attention(to_np(qd), to_np(kd), to_np(vd), scale) / v_scale
+    err = attention_errors(got, exact)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+
+
 @pytest.mark.parametrize("head_dim", [128, 256])
 def test_outlier_with_correction_phase(cuda, head_dim):
     """The same late outlier with pruning and mean correction on (alpha 0.5):

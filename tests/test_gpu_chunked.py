@@ -139,11 +139,53 @@ def test_chunk_shorter_than_a_tile_is_exact_causal(cuda):
                         collect_stats=True)
     cp.step(q[:, :1280], k[:, :1280], v[:, :1280])
     assert cp.block_sparsity() > 0  # the long chunk prunes
+    sparsity, visible = cp.block_sparsity(), cp._visible
     short = cp.step(q[:, 1280:1300], k[:, 1280:1300], v[:, 1280:1300])
     torch.cuda.synchronize()
+    # the hook's accounting leaves such a call out (patch.py:255-266)
+    assert cp._visible == visible and cp.block_sparsity() == sparsity
     exact = orc.exact_causal_attention(to_np(q[:, 1280:1300]), to_np(k[:, :1300]),
                                        to_np(v[:, :1300]), 128 ** -0.5, offset=1280)
     err = attention_errors(to_np(short[0]), exact)
+    assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, err
+
+
+def test_prefix_past_the_block_limit_is_exact_causal(cuda):
+    """A prefix of 8193 key blocks (past the selection kernel's limit, where
+    the hook hands the call to the original attention) runs exact causal
+    attention: every visible block, in order, through the attention kernel.
+    Checked against float32 attention on the GPU (float32 products only)
+    and counted as dense.  The chunked calls stay out of the hook's
+    ``block_sparsity``."""
+    from fpv2 import _lib, block_sparsity, disable, enable
+    lq = 32
+    total = _lib.MAX_BLOCKS * 128 + lq
+    cp = ChunkedPrefill(4, 1, 64, total, config=FPV2Config(alpha=0.5), min_tokens=1,
+                        device=cuda, collect_stats=True)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    k_rows, v_rows = cp.reserve(total - lq)
+    k_rows.copy_(torch.randn(k_rows.shape, generator=g, device=cuda))
+    v_rows.copy_(torch.randn(v_rows.shape, generator=g, device=cuda))
+    q = torch.randn((4, lq, 64), generator=g, device=cuda).bfloat16()
+    k = torch.randn((1, lq, 64), generator=g, device=cuda).bfloat16()
+    v = torch.randn((1, lq, 64), generator=g, device=cuda).bfloat16()
+    enable(min_tokens=1, collect_stats=True)
+    try:
+        keep = {}
+        cp.append(k, v)
+        out = cp.attend(q, keep=keep)[0]
+        torch.cuda.synchronize()
+        assert block_sparsity() == 0.0  # nothing counted by the hook
+    finally:
+        disable()
+    assert keep["lists"][0].shape[-1] == _lib.MAX_BLOCKS + 1
+    assert cp.block_sparsity() == 0.0 and cp._visible == _lib.MAX_BLOCKS + 1
+    kf, vf = cp.k[0].float(), cp.v[0].float()  # [total, 64]
+    s = (q.float() @ kf.T) * 0.125  # float32 on the GPU
+    mask = torch.arange(total, device=cuda)[None, :] <= (total - lq + torch.arange(lq, device=cuda))[:, None]
+    s = s.masked_fill(~mask[None], float("-inf"))
+    want = torch.softmax(s, dim=-1) @ vf
+    err = attention_errors(to_np(out), to_np(want))
     assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, err
 
 
@@ -152,8 +194,9 @@ def test_config4_chunked_65536_in_2048_token_chunks(cuda):
     2048-token chunks over a growing bf16 KV cache, ``total_tokens`` known.
     Every chunk equals the hook (``fpv2_sdpa``, which re-pools the whole
     prefix) bit for bit, the dense tail appears only on the last chunk, and
-    sampled tiles of the last chunk match the oracle on the full prefix:
-    block lists outside the 1e-4 band and rows within 2e-2 / 2e-3."""
+    sampled tiles of the last chunk and of a middle chunk match the oracle on
+    their full prefixes: block lists outside the 1e-4 band and rows within
+    2e-2 / 2e-3."""
     from fpv2.synthetic import baseline_qkv
     total, chunk = 65536, 2048
     q, k, v = baseline_qkv(total, planted=3.0, heavy_fraction=0.06, seed=0, device=cuda)
@@ -161,6 +204,7 @@ def test_config4_chunked_65536_in_2048_token_chunks(cuda):
     cp = ChunkedPrefill(32, 8, 128, total, config=config, total_tokens=total, min_tokens=2048,
                         device=cuda)
     keep = None
+    middle = None
     for s0 in range(0, total, chunk):
         s1 = s0 + chunk
         cp.append(k[:, s0:s1], v[:, s0:s1])
@@ -171,19 +215,34 @@ def test_config4_chunked_65536_in_2048_token_chunks(cuda):
         ref = fpv2_sdpa(q[None, :, s0:s1], k[None, :, :s1], v[None, :, :s1], scale=128 ** -0.5,
                         config=cp.request_config(chunk))
         assert torch.equal(out, ref), (s0, s1)
+        if s1 == total // 2:
+            middle = (keep, out, s0)
     torch.cuda.synchronize()
-    cfg = keep["config"]
-    tq, off = cfg.tile_q, total - chunk
-    ids, counts, _, _ = keep["lists"]
-    nb = ids.shape[-1]
+    kn, vn = to_np(k), to_np(v)
+    nb = keep["lists"][0].shape[-1]
     pooled_k = to_np(cp.pooled_k[:, :nb])
     pooled_v = to_np(cp.pooled_v[:, :nb])
-    kn, vn = to_np(k), to_np(v)
     assert np.array_equal(pooled_k, orc.pool_blocks(kn, 128, out_dtype="bf16"))
     assert np.array_equal(pooled_v, orc.pool_blocks(vn, 128, out_dtype="bf16"))
+    # the last chunk (dense tail) and a middle one (chunk 15 of 32, keys up
+    # to 32768, no tail: total_tokens not reached) against the oracle on
+    # their full prefixes; blocks pooled once are the same in both caches
+    for keep_c, out_c, off in ((keep, out, total - chunk), middle):
+        _check_chunk_tiles(q, kn, vn, keep_c, out_c, off, chunk, pooled_k, pooled_v)
+
+
+def _check_chunk_tiles(q, kn, vn, keep, out, off, chunk, pooled_k, pooled_v):
+    """Start, middle and end tiles of one chunk's call (queries at ``off``)
+    against the oracle: lists outside the 1e-4 band, rows on the device's
+    selection."""
+    cfg = keep["config"]
+    tq = cfg.tile_q
+    ids, counts, _, _ = keep["lists"]
+    nb = ids.shape[-1]
+    pooled_k, pooled_v = pooled_k[:, :nb], pooled_v[:, :nb]
     ocfg = orc.OracleConfig(**{f: getattr(cfg, f) for f in orc.OracleConfig.__dataclass_fields__})
     nt = chunk // tq
-    for t0, n in ((0, 2), (nt // 2, 2), (nt - 3, 3)):  # start, middle, end (dense tail)
+    for t0, n in ((0, 2), (nt // 2, 2), (nt - 3, 3)):  # start, middle, end
         rows0 = t0 * tq
         qs = to_np(q[:, off + rows0:off + rows0 + n * tq])
         # the sampled tiles as their own call at offset off + rows0; the dense
@@ -198,9 +257,10 @@ def test_config4_chunked_65536_in_2048_token_chunks(cuda):
             for t in range(n):
                 dev_sel[h, t, idn[h, t, :cn[h, t]]] = True
         decided = np.abs(ratio - cfg.alpha) > 1e-4
-        assert np.array_equal(sel[decided], dev_sel[decided]), t0
+        assert np.array_equal(sel[decided], dev_sel[decided]), (off, t0)
         ref = orc.fpv2_attention_blockwise(
-            qs, kn, vn, scale=128 ** -0.5, selected=dev_sel, pooled_k=pooled_k,
-            pooled_v=pooled_v, config=sub_cfg, offset=off + rows0, row_block=tq)
+            qs, kn[:, :off + chunk], vn[:, :off + chunk], scale=128 ** -0.5, selected=dev_sel,
+            pooled_k=pooled_k, pooled_v=pooled_v, config=sub_cfg, offset=off + rows0,
+            row_block=tq, key_length=off + chunk)
         err = attention_errors(to_np(out[0, :, rows0:rows0 + n * tq]), ref)
-        assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (t0, err)
+        assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (off, t0, err)

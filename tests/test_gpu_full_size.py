@@ -4,9 +4,10 @@ The hook runs the whole layer (Qwen3-4B geometry, BASELINE generator) on the
 GPU at seq 32768 and 131072; the oracle then checks, from the same inputs:
   * the pooled K/V of the whole layer, bit-exact against the oracle's pooling
     of the full K/V;
-  * block lists of sampled query tiles (from the start, the middle and the
-    end of the call; at 32k, every tile) bit-exact against the oracle's
-    selection, excluding blocks whose energy ratio lies within 1e-4 of alpha;
+  * the block lists of every query tile bit-exact against the oracle's
+    selection (scored on the host's cores over tile ranges), excluding
+    blocks whose energy ratio lies within 1e-4 of alpha, and the full
+    padded selected/pruned lists against the oracle's compaction;
   * the attention rows of the sampled tiles within max-abs 2e-2 / mean-abs
     2e-3 of the oracle's blockwise float32 evaluation on the device's
     selection.
@@ -22,7 +23,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import attention_errors, to_np
+from conftest import attention_errors, oracle_select_parallel, to_np
 from oracle import fpv2_oracle as orc
 from fpv2 import FPV2Config
 from fpv2.patch import _fpv2_sdpa
@@ -80,6 +81,28 @@ def _check_tiles(q, kn, vn, out, keep, seq, samples, *, sparse=False):
         assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, (t0, n, err)
 
 
+def _check_every_list(q, keep, seq):
+    """Every tile x KV head of a call whose queries start at key 0: lists
+    outside the 1e-4 band against the oracle's selection, and the full padded
+    lists (selected ascending, then the rest), counts and pruned lists equal
+    to the oracle's compaction of the device's mask."""
+    cfg = keep["config"]
+    ids, counts, pids, pcounts = keep["lists"]
+    nb, nt = ids.shape[-1], ids.shape[1]
+    dev_sel = _device_mask(ids, counts, slice(0, nt), nb)
+    sel, ratio = oracle_select_parallel(to_np(q), to_np(keep["pooled_k"]), scale=SCALE,
+                                        config=_oracle_config(cfg), offset=0, query_length=seq)
+    decided = np.abs(ratio - cfg.alpha) > BAND
+    assert np.array_equal(sel[decided], dev_sel[decided])
+    o_ids, o_counts, o_pids, o_pcounts = orc.compact_block_indices(
+        dev_sel, config=_oracle_config(cfg), offset=0, query_length=seq, key_length=seq)
+    assert np.array_equal(to_np(ids), o_ids) and np.array_equal(to_np(counts), o_counts)
+    assert np.array_equal(to_np(pcounts), o_pcounts)
+    head = np.arange(nb)[None, None, :] < o_pcounts[..., None]  # the defined entries
+    assert np.array_equal(np.where(head, to_np(pids), -1), np.where(head, o_pids, -1))
+    return int(decided.sum())
+
+
 def _samples(nt, n_end):
     """Tile groups from the start, the middle and the end of the call."""
     return ((0, 2), (nt // 2, 2), (nt - n_end, n_end))
@@ -107,6 +130,7 @@ def test_sampled_tiles_match_oracle_at_full_size(cuda, seq, heavy, planted, alph
     assert np.array_equal(to_np(keep["pooled_v"]), orc.pool_blocks(vn, 128, out_dtype="bf16"))
     nt = seq // keep["config"].tile_q
     _check_tiles(q, kn, vn, out, keep, seq, _samples(nt, n_end), sparse=planted > 3.0)
+    assert _check_every_list(q, keep, seq) > 0.99 * 8 * nt * (nt * 32 // 128 + 1) / 2
 
 
 def test_every_tile_list_at_32k_matches_oracle(cuda):

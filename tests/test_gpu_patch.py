@@ -19,7 +19,7 @@ import torch.nn.functional as F
 from conftest import attention_errors, to_np
 from oracle import fpv2_oracle as orc
 from fpv2 import FPV2Config, block_sparsity, disable, enable, fpv2_sdpa
-from fpv2.patch import _ORIGINAL_SDPA, _request_config
+from fpv2.patch import _ORIGINAL_SDPA, _fpv2_sdpa, _request_config
 from fpv2.synthetic import baseline_qkv, structured_qkv
 
 pytestmark = pytest.mark.gpu
@@ -171,9 +171,38 @@ def _baseline_parity(cuda, seq, planted, tiles):
 
 
 def test_baseline_config1_8k_matches_oracle(cuda):
+    """BASELINE config 1 through the hook: sampled rows against the oracle's
+    hook data flow, and every tile's block lists (256 tiles x 8 KV heads)
+    against the oracle's selection and compaction, bit for bit outside the
+    1e-4 band."""
     nt = 8192 // 32
     tiles = sorted({0, 1, 2, 3, 100, 177, nt // 2, nt - 3, nt - 2, nt - 1})
     _baseline_parity(cuda, 8192, 3.0, tiles)
+    q, k, v = baseline_qkv(8192, planted=3.0, heavy_fraction=0.06, seed=0)
+    keep = {}
+    config = FPV2Config(alpha=0.1, sink_tokens=128)
+    _fpv2_sdpa(q[None].to(cuda), k[None].to(cuda), v[None].to(cuda), scale=128 ** -0.5,
+               config=config, keep=keep)
+    torch.cuda.synchronize()
+    ids, counts, pids, pcounts = (to_np(x) for x in keep["lists"])
+    plan_cfg = orc.OracleConfig(**{f: getattr(keep["config"], f)
+                                   for f in orc.OracleConfig.__dataclass_fields__})
+    sel, _, ratio = orc.block_scores_and_select(
+        to_np(q), to_np(keep["pooled_k"]), scale=128 ** -0.5,
+        config=orc._replace(plan_cfg, score_chunk_tiles=32), return_ratio=True)
+    dev_sel = np.zeros(sel.shape, dtype=bool)
+    for h in range(ids.shape[0]):
+        for t in range(ids.shape[1]):
+            dev_sel[h, t, ids[h, t, :counts[h, t]]] = True
+    decided = np.abs(ratio - 0.1) > 1e-4
+    assert decided.sum() > 0.99 * decided.size
+    assert np.array_equal(sel[decided], dev_sel[decided])
+    o_ids, o_counts, o_pids, o_pcounts = orc.compact_block_indices(
+        dev_sel, config=plan_cfg, query_length=8192, key_length=8192)
+    assert np.array_equal(ids, o_ids) and np.array_equal(counts, o_counts)
+    assert np.array_equal(pcounts, o_pcounts)
+    head = np.arange(ids.shape[-1])[None, None, :] < o_pcounts[..., None]
+    assert np.array_equal(np.where(head, pids, -1), np.where(head, o_pids, -1))
 
 
 def test_baseline_contrast_variant_exercises_pruning(cuda):
@@ -187,21 +216,49 @@ def test_baseline_contrast_variant_exercises_pruning(cuda):
 
 def test_block_counter_waits_for_the_stream_that_wrote_the_counts(cuda):
     """Counts written on a side stream (behind a long matmul) are summed on
-    the default stream: the fold waits for the side stream."""
+    the default stream: the fold waits for the side stream.  Folds happen on
+    two different streams, so the running total itself moves between them."""
     from fpv2.patch import SelectedBlockCounter
     counter = SelectedBlockCounter(fold_every=4)
     side = torch.cuda.Stream(device=cuda)
+    other = torch.cuda.Stream(device=cuda)
     a = torch.randn((4096, 4096), device=cuda)
     torch.cuda.synchronize()
     expected = 0
-    with torch.cuda.stream(side):
-        for i in range(6):
-            b = a @ a  # keeps the side stream busy before each count is written
-            counts = torch.full((2, 8), i + 1, dtype=torch.int32, device=cuda)
-            counts += (b[0, :1] * 0).to(torch.int32)  # written after the matmul
-            counter.add(counts)
-            expected += 16 * (i + 1)
+    for stream in (side, other, side):
+        with torch.cuda.stream(stream):
+            for i in range(6):
+                b = a @ a  # keeps the stream busy before each count is written
+                counts = torch.full((2, 8), i + 1, dtype=torch.int32, device=cuda)
+                counts += (b[0, :1] * 0).to(torch.int32)  # written after the matmul
+                counter.add(counts)  # folds every 4 calls, on this stream
+                expected += 16 * (i + 1)
+            # memory the allocator may hand to the next counts on this stream
+            junk = torch.full((1 << 20,), -7, dtype=torch.int64, device=cuda)
+            del junk
     assert counter.value() == expected
+
+
+def test_calls_past_the_block_limit_reach_the_original_sdpa(cuda):
+    """An otherwise eligible call whose keys need 8193 blocks (one more than
+    the selection kernel holds) is served by the original SDPA, bit for bit,
+    and counted as dense; the reference's hook has no such limit and serves
+    every eligible call (patch.py:237-271), so the call is not refused."""
+    from fpv2 import _lib
+    lq, lk = 32, _lib.MAX_BLOCKS * 128 + 1
+    g = torch.Generator(device=cuda).manual_seed(5)
+    q = torch.randn((1, 4, lq, 64), generator=g, device=cuda).bfloat16()
+    k = torch.randn((1, 1, lk, 64), generator=g, device=cuda).bfloat16()
+    v = torch.randn((1, 1, lk, 64), generator=g, device=cuda).bfloat16()
+    kwargs = dict(attn_mask=causal_lower_right(lq, lk), scale=0.125, enable_gqa=True)
+    expected = _ORIGINAL_SDPA(q, k, v, **kwargs)
+    enable(min_tokens=1, collect_stats=True)
+    actual = F.scaled_dot_product_attention(q, k, v, **kwargs)
+    torch.cuda.synchronize()
+    assert torch.equal(actual, expected)
+    assert block_sparsity() == 0.0
+    from fpv2 import patch
+    assert patch._visible_blocks == patch._selected_dense_blocks == _lib.MAX_BLOCKS + 1
 
 
 @pytest.mark.parametrize(("heads", "dim"), [((32, 2), 128), ((64, 2), 64), ((32, 1), 128)])

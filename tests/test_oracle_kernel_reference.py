@@ -191,3 +191,43 @@ def test_blockwise_equals_literal_reference():
     blk = orc.fpv2_attention_blockwise(q, k, v, scale=0.125, selected=sel, pooled_k=pk,
                                        pooled_v=pv, config=cfg, dtype=np.float64, row_block=64)
     assert np.allclose(lit, blk, rtol=1e-9, atol=1e-12)
+
+
+@pytest.mark.parametrize(("offset", "qlen", "workers"), [(0, 1024, 3), (200, 937, 4), (0, 64, 2)])
+def test_tile_range_evaluation_equals_one_call(offset, qlen, workers):
+    """Selection and attention of a whole call, evaluated as calls of tile
+    ranges on several threads, equal the one-call oracle: the selection bit
+    for bit (the dense tail, last 2 tiles, stays with the call's end; offsets
+    and the partial last tile carry over), the attention up to float32
+    summation order (rows are grouped into different BLAS products)."""
+    rng = np.random.default_rng(offset + qlen)
+    hq, hkv, d, tq, bk = 4, 2, 32, 32, 64
+    lq_pad = -(-qlen // tq) * tq
+    nb = -(-(offset + lq_pad) // bk)
+    q = rng.standard_normal((hq, lq_pad, d)).astype(np.float32)
+    q[:, qlen:] = 0
+    k = rng.standard_normal((hkv, nb * bk, d)).astype(np.float32)
+    v = rng.standard_normal((hkv, nb * bk, d)).astype(np.float32)
+    k[:, :bk] += 2.0
+    lk = offset + qlen
+    k[:, lk:] = 0
+    v[:, lk:] = 0
+    cfg = orc.OracleConfig(block_k=bk, tile_q=tq, alpha=0.2, sink_tokens=bk, window_tokens=bk)
+    pk = orc.pool_blocks(k, bk, out_dtype="bf16")
+    pv = orc.pool_blocks(v, bk, out_dtype="bf16")
+    one, _, ratio = orc.block_scores_and_select(
+        q, pk, scale=d ** -0.5, config=orc._replace(cfg, score_chunk_tiles=5), offset=offset,
+        query_length=qlen, return_ratio=True)
+    sel, ratio2 = orc.select_tile_ranges(q, pk, scale=d ** -0.5, config=cfg, offset=offset,
+                                         query_length=qlen, workers=workers)
+    assert np.array_equal(sel, one) and np.array_equal(ratio, ratio2)
+    if nb > 4:
+        assert sel[:, -1].sum() > sel[:, 0].sum()  # the dense tail is present
+    want = orc.fpv2_attention_blockwise(q, k, v, scale=d ** -0.5, selected=one, pooled_k=pk,
+                                        pooled_v=pv, config=cfg, offset=offset,
+                                        query_length=qlen, key_length=lk)
+    got = orc.attention_tile_ranges(q, k, v, scale=d ** -0.5, selected=one, pooled_k=pk,
+                                    pooled_v=pv, config=cfg, offset=offset, query_length=qlen,
+                                    key_length=lk, workers=workers)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+    assert not np.array_equal(got[:, :qlen], 0)
