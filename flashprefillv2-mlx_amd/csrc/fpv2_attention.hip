@@ -14,11 +14,14 @@
 //     (128 rows, two workgroups per CU); D = 256 uses 8 waves for the same
 //     rows, two per 32-row group, each owning half of the head dimension
 //     for the products and half of each slice's keys for the softmax;
-//   * each wave owns 32 query rows; Q lives in VGPRs for the whole walk;
-//   * S^T = K . Q^T with v_mfma_f32_32x32x16_{bf16,f16}: lane l owns query
-//     row l%32 and 16 of the 32 keys of each key tile, so row max/sum need a
-//     single lane-pair exchange and P feeds the next MFMA without a transpose;
-//   * O^T = V^T . P^T: the rescale by exp2(m_old - m_new) is lane-local;
+//   * each wave owns 32 query rows, two 16-row tiles; Q lives in VGPRs for
+//     the whole walk;
+//   * S^T = K . Q^T with v_mfma_f32_16x16x32_{bf16,f16} (2 x 2 tiles of 16
+//     keys x 16 rows per 32-key slice): lane l owns query row l%16 of each
+//     row tile and keys 4(l/16).. of each key tile, so row max/sum need two
+//     lane exchanges and P feeds the PV MFMA without a transpose;
+//   * O^T = V^T . P^T, each V^T fragment read once for both row tiles: the
+//     rescale by exp2(m_old - m_new) is lane-local;
 //   * K/V sub-tiles of 32 keys stream through a ring of NST LDS stages
 //     filled by buffer_load_dwordx4 ... lds, NST-2 sub-tiles ahead of the
 //     multiply; LDS rows are unpadded with an XOR swizzle of their
@@ -66,29 +69,37 @@ __device__ __forceinline__ void lgkm_wait(u32x2 (&r)[8]) {
 }
 // In-place multiply; keeps a conditionally rescaled MFMA accumulator in its
 // registers instead of a copy per branch.
-__device__ __forceinline__ void scale_in_place(f32x16& acc, float f) {
+__device__ __forceinline__ void scale_in_place(f32x4& acc, float f) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 4; ++j) {
     float x = acc[j];
     asm volatile("v_mul_f32 %0, %0, %1" : "+v"(x) : "v"(f));
     acc[j] = x;
   }
 }
 
-// max / sum of x over the lane pair (l, l ^ 32), one v_permlane32_swap_b32:
-// the two halves of the swap hold x of both lanes of the pair in either order.
-__device__ __forceinline__ float pair_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+// max / sum of x over the four lanes l ^ {0, 16, 32, 48} that hold one row
+// of a 16x16 accumulator: v_permlane16_swap_b32 then v_permlane32_swap_b32,
+// whose two results hold x of both lanes of each pair in either order.
+__device__ __forceinline__ float quad_max(float x) {
   // plain v_max_f32: the operands are MFMA results or -inf, never signalling
   // NaNs, so the canonicalising form fmaxf() would add is not needed
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   float m;
-  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(r[0])), "v"(__uint_as_float(r[1])));
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(a[0])), "v"(__uint_as_float(a[1])));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  asm("v_max_f32 %0, %1, %2" : "=v"(m) : "v"(__uint_as_float(b[0])), "v"(__uint_as_float(b[1])));
   return m;
 }
-__device__ __forceinline__ float pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+// (the pair sums are added in the same order in all four lanes, so they
+// hold the same value)
+__device__ __forceinline__ float quad_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 
 struct AttnArgs {
@@ -129,9 +140,10 @@ __device__ __forceinline__ int clampi(int x, int lo, int hi) {
 
 // LDS geometry of one K or V sub-tile: BN rows of ROWB bytes (D elements
 // padded to a power of two), 16-byte chunk c of row r stored at chunk
-// c ^ mask(r).  The masks make the 16 rows of a ds_read_b128 quarter-wave hit
-// 16 different 16-byte bank groups, and the 4 rows of a transposing read
-// group 4 different 64-byte bank quarters.
+// c ^ mask(r).  The masks make the 16 rows of a ds_read_b128 quarter-wave
+// (16 keys, one chunk) hit 16 different 16-byte bank groups, and the 8 rows
+// of each half of a transposing read (8 keys x 32 bytes of one d-tile) hit 8
+// different 32-byte bank groups.
 template <int D>
 struct Geom {
   static constexpr int ROWB = D <= 64 ? 128 : (D <= 128 ? 256 : 512);
@@ -142,13 +154,14 @@ struct Geom {
   static constexpr int STAGE = 2 * TILE;   // K then V
   static constexpr int JT = TILE / 1024;   // fill instructions (64 lanes x 16 B) per sub-tile
   static constexpr int RPI = 64 / RC;      // rows per fill instruction
-  static constexpr int KS = D / 16;        // QK^T k-steps
-  static constexpr int DT = D / 32;        // O^T row tiles (32 dims)
+  static constexpr int KS = D / 32;        // QK^T k-steps (32 dims each)
+  static constexpr int DT = D / 16;        // O^T d-tiles (16 dims each)
   static __device__ __forceinline__ int kmask(int row) {
     return ROWB >= 256 ? (row & 15) : ((row >> 1) & 7);
   }
+  // (even: chunk pairs stay pairs; rows of one 256-byte span apart)
   static __device__ __forceinline__ int vmask(int row) {
-    return ROWB >= 256 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+    return ROWB >= 256 ? ((row & 7) << 1) : (((row >> 1) & 3) << 1);
   }
 };
 
@@ -172,38 +185,39 @@ struct Step {
 template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
 __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D>;
-  static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0), "D split in halves");
-  // 32-row groups per wave: one.  The per-row-group arrays below keep the
-  // row group as their first index.
-  constexpr int RG = 1;
+  constexpr int RT = 2;  // 16-row query tiles per wave (32 rows)
+  constexpr int KT = 2;  // 16-key tiles per slice (32 keys)
+  static_assert(DS == 1 || (DS == 2 && WAVES % 2 == 0 && GM::DT % 2 == 0 && GM::KS % 2 == 0),
+                "D split in halves");
   // asm LDS reads unless a wave's registers do not hold them (D = 256 without
   // the split), where the compiler schedules its LDS reads (see lds_read_b128).
   constexpr bool kAsm = D <= 128 || DS == 2;
-  constexpr int DT = GM::DT / DS;  // 32-wide output column tiles of this wave
-  constexpr int KSQ = GM::KS / DS; // 16-deep QK k-steps of this wave
-  // DS = 2: S element j < 8 of a wave holds one of its own 16 keys (keys
-  // 0-15 for the first wave of the pair, 16-31 for the second, which reads
-  // its K rows rotated by 16); elements 8-15 hold the partner's keys.
+  constexpr int DT = GM::DT / DS;  // 16-wide output d-tiles of this wave
+  constexpr int KSQ = GM::KS / DS; // 32-deep QK k-steps of this wave
+  constexpr int KR = 2 * KSQ;      // K fragment reads per slice: (k-step, key tile)
+  // DS = 2: the first wave of a pair owns key tile 0 (keys 0-15 of each
+  // slice), the second key tile 1 (keys 16-31).
   constexpr bool KSPLIT = DS == 2;
   using vec8 = typename Elem<T>::vec8;
   constexpr int BN = GM::BN;
   constexpr int ROWB = GM::ROWB;
-  constexpr int RW = WAVES / DS * 32 * RG;  // packed query rows per workgroup
+  constexpr int RW = WAVES / DS * 32;     // packed query rows per workgroup
   constexpr int NIK = GM::JT / WAVES;     // fill instructions per wave per sub-tile
   constexpr int NI = 2 * NIK;             // ... per stage (K then V)
   static_assert(GM::JT % WAVES == 0, "fills must split evenly over the waves");
   static_assert(NST >= 2 && NI * (NST - 2) <= 63, "vmcnt range");
   // the stage ring, then (DS = 2) 4 KiB per wave for its partner: bytes
-  // [0, 1024) its P (16 bytes per lane), [1024, 1280) a float per lane (row
-  // max, row sum), [2048, 4096) its partial S of the partner's keys
+  // [0, 1024) its P (16 bytes per lane), [1024, 1536) two floats per lane
+  // (row max or row sum of both row tiles), [2048, 4096) its partial S of
+  // the partner's key tile
   __shared__ __align__(1024) uint8_t smem[NST * GM::STAGE + (DS == 2 ? WAVES * 4096 : 0)];
   uint8_t* const xbuf = smem + NST * GM::STAGE;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
-  const int l32 = lane & 31;
-  const int hf = lane >> 5;
+  const int l16 = lane & 15;
+  const int grp = lane >> 4;  // 16-lane group: keys 4*grp.. of each key tile
 
   // ---- workgroup -> (KV head, tile, row chunk); latest tiles first ----
   const int bid = blockIdx.x;
@@ -215,24 +229,25 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const int last_local = min((t + 1) * a.tq, a.Lq);
   const int abs_last = a.offset + last_local - 1;
 
-  // ---- this lane's query rows (one per row group of the wave) ----
+  // ---- this lane's query rows: row l16 of each of the wave's two 16-row
+  // tiles (the S^T / O^T column the lane holds) ----
   const int R = a.G * a.tq;
-  const int rwave = wave % (WAVES / DS);  // row groups of this wave
+  const int rwave = wave % (WAVES / DS);  // 32-row group of this wave
   const int dhalf = wave / (WAVES / DS);  // part of the head dimension (DS = 2)
-  bool exists[RG], row_valid[RG];
-  int g[RG], pos[RG], qpos_abs[RG];
+  bool exists[RT], row_valid[RT];
+  int g[RT], pos[RT], qpos_abs[RT];
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
-    const int prow = chunk * RW + (rwave * RG + rg) * 32 + l32;
-    exists[rg] = prow < R;
-    g[rg] = 0;
-    pos[rg] = 0;
-    if (exists[rg]) {
-      g[rg] = prow / a.tq;
-      pos[rg] = t * a.tq + (prow - g[rg] * a.tq);
+  for (int rt = 0; rt < RT; ++rt) {
+    const int prow = chunk * RW + rwave * 32 + rt * 16 + l16;
+    exists[rt] = prow < R;
+    g[rt] = 0;
+    pos[rt] = 0;
+    if (exists[rt]) {
+      g[rt] = prow / a.tq;
+      pos[rt] = t * a.tq + (prow - g[rt] * a.tq);
     }
-    row_valid[rg] = exists[rg] && pos[rg] < a.Lq;
-    qpos_abs[rg] = a.offset + pos[rg];
+    row_valid[rt] = exists[rt] && pos[rt] < a.Lq;
+    qpos_abs[rt] = a.offset + pos[rt];
   }
 
   // bfloat16 (8 exponent bits, like float32) takes the reference-free first
@@ -243,7 +258,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // float16 P (5 exponent bits) needs a reference: its first pass takes
   // each row's max over its first slice and P = exp2(s*c - m_ref).
   constexpr bool kFree = std::is_same<T, bf16_t>::value;
-  vec8 qf[RG][KSQ];
+  // Q^T fragments (the B operand): lane l holds 8 consecutive dims
+  // 32k + 8*grp.. of its row in each row tile
+  vec8 qf[RT][KSQ];
   {
     const rsrc_t qr = make_rsrc(a.q + static_cast<int64_t>(h) * a.G * a.q_hs, a.q_bytes);
     // float16: the softmax folds the scale into one FMA per logit and needs
@@ -251,14 +268,14 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // (s*c = (-s)*(-c)).
     const uint32_t sign = (!kFree && a.c_scale < 0.f) ? 0x80008000u : 0u;
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
+    for (int rt = 0; rt < RT; ++rt) {
       const uint32_t qoff =
-          row_valid[rg]
-              ? static_cast<uint32_t>((g[rg] * a.q_hs + static_cast<int64_t>(pos[rg]) * a.q_rs + hf * 8) * 2)
+          row_valid[rt]
+              ? static_cast<uint32_t>((g[rt] * a.q_hs + static_cast<int64_t>(pos[rt]) * a.q_rs + grp * 8) * 2)
               : kOOB;
 #pragma unroll
       for (int k = 0; k < KSQ; ++k) {
-        u32x4 v = buf_load16(qr, qoff + (row_valid[rg] ? (dhalf * KSQ + k) * 32 : 0));
+        u32x4 v = buf_load16(qr, qoff + (row_valid[rt] ? (dhalf * KSQ + k) * 64 : 0));
         if constexpr (kFree) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -267,7 +284,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
         } else {
           v ^= sign;
         }
-        qf[rg][k] = as_vec8<T>(v);
+        qf[rt][k] = as_vec8<T>(v);
       }
     }
   }
@@ -510,68 +527,63 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // O / l are rescaled only when some row's max grows past that, so the
   // common case costs no rescale at all.  The result O / l is unchanged.
   constexpr float kRescaleSlack = 8.0f;
-  f32x16 o[RG][DT];
+  // O^T tiles: o[dt][rt] holds dims 16dt + 4grp + 0..3 of the lane's row of
+  // row tile rt (a 16x16 accumulator of v_mfma_f32_16x16x32)
+  f32x4 o[DT][RT];
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
+  for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-    for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
+    for (int rt = 0; rt < RT; ++rt) o[dt][rt] = f32x4{};
   }
-  float m_ref[RG];
+  float m_ref[RT];
   // Derived from m_ref, updated only when it changes: the exp2 bias
   // (-m_ref, 0 while no key has been seen) and the rescale threshold.  The
   // kernels without correction, and those with D = 256, are at the register
   // limit and recompute them per slice instead of keeping two more live values.
   constexpr bool kKeepRef = CORR && D <= 128;
-  float neg_m[RG], m_thr[RG], l_run[RG];
+  float neg_m[RT], m_thr[RT], l_run[RT];
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
-    m_ref[rg] = neg_inf();
-    neg_m[rg] = 0.f;
-    m_thr[rg] = neg_inf();
-    l_run[rg] = 0.f;
+  for (int rt = 0; rt < RT; ++rt) {
+    m_ref[rt] = neg_inf();
+    neg_m[rt] = 0.f;
+    m_thr[rt] = neg_inf();
+    l_run[rt] = 0.f;
   }
-  auto bias_of_ref = [&](int rg) {
-    return kKeepRef ? neg_m[rg] : ((m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg]);
+  auto bias_of_ref = [&](int rt) {
+    return kKeepRef ? neg_m[rt] : ((m_ref[rt] == neg_inf()) ? 0.f : -m_ref[rt]);
   };
-  auto thr_of_ref = [&](int rg) { return kKeepRef ? m_thr[rg] : m_ref[rg] + kRescaleSlack; };
+  auto thr_of_ref = [&](int rt) { return kKeepRef ? m_thr[rt] : m_ref[rt] + kRescaleSlack; };
 
-  // LDS read addresses relative to a slice (32 keys of a stage).  K: lane
-  // reads row l32, data chunk 2k + hf -> kbase ^ 32k.  V^T: lane j of a
-  // 16-lane group reads row (j/4) and dims 4*(j%4).. of a 4-key x 16-dim
-  // patch (the transpose hands lane i the 4 keys of dim d0 + i): rows
-  // 16u + 4hf + (lane&15)/4 (+8), dims 32dt + ... -> (vbase ^ 64dt) +
-  // (16u (+8)) * ROWB.  The XOR terms only touch bits below 9, and slice
-  // offsets are multiples of 32 rows, so slice offsets add outside the XOR.
-  // (DS = 2: the second wave of a pair reads key row l32 ^ 16, which has the
-  // same swizzle, so its S elements 0-7 hold keys 16-31)
-  const int krow = KSPLIT ? (l32 ^ (16 * dhalf)) : l32;
-  const int km = GM::kmask(krow);
-  // (DS = 2: this wave's k-steps start 32*KSQ bytes along the row, above
-  // the swizzled bits)
-  const uint32_t kbase =
-      (smem_lds + krow * ROWB + ((16 * hf) ^ (16 * km))) ^ static_cast<uint32_t>(dhalf * KSQ * 32);
-  const int tr_row = (lane & 15) >> 2;
-  const int cig = ((lane >> 4) & 1) * 2 + ((lane & 3) >> 1);  // chunk within a 64-byte group
-  const int vq = ROWB >= 256 ? tr_row : ((tr_row >> 1) & 1);   // swizzled 64-byte group
-  // (DS = 2: the second half of D lies 64*DT bytes further along each row,
-  // above the swizzled bits)
-  const uint32_t vbase =
-      (smem_lds + GM::TILE + (hf * 4 + tr_row) * ROWB + vq * 64 + cig * 16 + (lane & 1) * 8) ^
-      static_cast<uint32_t>(dhalf * DT * 64);
-  // DS = 2: V^T rows of the wave's own 16 keys (first P operand) and of the
-  // partner's (second), 16 rows apart; the swizzle repeats every 4 rows.
-  const uint32_t vbase_own = vbase + (KSPLIT ? dhalf * 16 * ROWB : 0);
-  const uint32_t vbase_oth = vbase + (KSPLIT ? (1 - dhalf) * 16 * ROWB : 0);
+  // LDS read addresses relative to a slice (32 keys of a stage).
+  // K, the A operand of S^T = K . Q'^T: lane l reads key row l16 (+16 rows,
+  // an immediate offset, for key tile 1) and the 16-byte chunk 4k + grp of
+  // k-step k, stored at chunk (4k + grp) ^ kmask = 4k ^ (grp ^ kmask):
+  // kbase ^ 64k.  V^T, the A operand of O^T = V^T . P^T: lane i of 16-lane
+  // group grp receives the 4 keys 4grp.. (and 16 + 4grp..) of dim 16dt + i;
+  // lane m of the group addresses key row 4grp + m/4 and the 8 bytes of dims
+  // 16dt + 4(m%4).., chunk (2dt + (m%4)/2) ^ vmask = 2dt ^ ((m%4)/2 ^ vmask):
+  // vbase ^ 32dt.  The XOR terms touch address bits 4-7 only, and slice
+  // offsets (whole stages) and the key-tile and D-half offsets lie above
+  // them.  (DS = 2: this wave's k-steps and d-tiles start KSQ*64 and DT*32
+  // bytes along the row, and its own key tile, read first, 16*dhalf rows
+  // in; the partner's tile is 16 rows away, an XOR of the 16*ROWB bit.)
+  const int km = GM::kmask(l16);
+  const int own = KSPLIT ? 16 * dhalf : 0;
+  const uint32_t kbase = smem_lds + (own + l16) * ROWB + (grp ^ km) * 16 + dhalf * KSQ * 64;
+  const int vrow = 4 * grp + (l16 >> 2);
+  const int vm = GM::vmask(vrow);
+  const uint32_t vbase = smem_lds + GM::TILE + (own + vrow) * ROWB + (((l16 & 3) >> 1) ^ vm) * 16 +
+                         (l16 & 1) * 8 + dhalf * DT * 32;
 
   // ---- slice pipeline ----
   // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
   // stages, one process() call apart, so that every stage pairs MFMA work
   // with VALU work of another slice:
-  //   A: S^T = K . Q^T of slice n       ||  exp2 / pack / row sum of 6 of
-  //                                          the 8 key pairs of slice n-1
+  //   A: S^T = K . Q'^T of slice n      ||  exp2 / pack / row sum of 6 of
+  //                                         the 8 key pairs of slice n-1
   //   B: O^T += V^T . P^T of slice n-1  ||  the last 2 key pairs (during the
-  //                                          MFMAs on the first P operand),
-  //                                          mask and row max of slice n
+  //                                         MFMAs of the first row tile),
+  //                                         mask and row max of slice n
   //   C: (rare) rescale of O and l when slice n raises the reference max.
   // A wave keeps its matrix pipe busy during its own softmax; the order of
   // issue within A and B is fixed in source order, each piece of VALU work
@@ -591,44 +603,43 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     return r;
   };
   // S^T of the slice between stages A and B of the pipeline (masked, its max
-  // folded into m_ref), in one of two buffers that alternate between slices.
-  f32x16 s_buf[2][RG];
+  // folded into m_ref), in one of two buffers that alternate between slices:
+  // s[rt][kt] holds keys 16kt + 4grp + 0..3 of the lane's row of row tile
+  // rt.  (DS = 2: s[rt][0] holds the wave's own key tile, s[rt][1] the
+  // partner's, whose partial this wave hands over.)
+  f32x4 s_buf[2][RT][KT];
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) s_buf[0][rg] = s_buf[1][rg] = f32x16{};
+  for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) s_buf[0][rt][kt] = s_buf[1][rt][kt] = f32x4{};
+  }
   Slice p_pend{0, 0, 0, 0u};
 
-  constexpr int PV_OPS = 2 * DT;  // PV MFMAs per slice: (u, dt)
   // issue-order tuning of the slice pipeline (see process_m)
-#ifndef FPV2_EXP_LEAD
-#define FPV2_EXP_LEAD 0
-#endif
-#ifndef FPV2_MAX_DELAY
-#define FPV2_MAX_DELAY 0
-#endif
-  constexpr int kExpLead = FPV2_EXP_LEAD;   // exp pairs issued before the first QK MFMA
 #ifndef FPV2_EXP_A
 #define FPV2_EXP_A 6
 #endif
-  // exp pairs of the pending slice in stage A; the rest (keys 16-31, the
-  // second P operand) are spread over the first half of the PV MFMAs
+  // exp pairs of the pending slice in stage A (the first row tile's four,
+  // then the second's); the rest are spread over the first row tile's PV
+  // MFMAs of the first V batch
   constexpr int kExpA = FPV2_EXP_A;
-  static_assert(kExpA >= 4 && kExpA <= 8, "the first P operand is built in stage A");
-  constexpr int kMaxDelay = FPV2_MAX_DELAY; // PV MFMAs issued before the first row-max step
-  constexpr int PER_BATCH = 4;        // MFMA operands per batch of 8 transposing reads
-  constexpr int BATCHES = (PV_OPS + PER_BATCH - 1) / PER_BATCH;
-  // (va: V^T rows of the first P operand's keys, va2: of the second's; with
-  // DS = 1 the second operand's rows follow at 16 rows from va)
-  auto issue_v = [&](uint32_t va, uint32_t va2, auto bc, u32x2 (&r)[8]) {
+  static_assert(kExpA >= 4 && kExpA <= 8, "the first row tile's P is built in stage A");
+  constexpr int PER_BATCH = 4;  // V^T fragments (d-tiles) per batch of 8 transposing reads
+  constexpr int BATCHES = (DT + PER_BATCH - 1) / PER_BATCH;
+  // V^T fragment of d-tile dt: the keys 4grp.. (slots 0-3 of the PV
+  // contraction) and 16 + 4grp.. (slots 4-7), as the P words are ordered.
+  // (DS = 2: slots 0-3 are the wave's own key tile, 16*dhalf + 4grp.., and
+  // slots 4-7 the partner's, so the second read flips the 16-row offset.)
+  auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8]) {
     constexpr int b = decltype(bc)::value;
     StaticFor<0, PER_BATCH>::run([&](auto qc) {
       constexpr int q = decltype(qc)::value;
-      constexpr int op = b * PER_BATCH + q;
-      if constexpr (op < PV_OPS) {
-        constexpr int u = op / DT, dt = op % DT;
-        constexpr int R0 = KSPLIT ? 0 : u * 16 * ROWB;
-        const uint32_t addr = ((KSPLIT && u == 1) ? va2 : va) ^ (64 * dt);
-        r[2 * q] = lds_read_tr<kAsm, R0>(addr);
-        r[2 * q + 1] = lds_read_tr<kAsm, R0 + 8 * ROWB>(addr);
+      constexpr int dt = b * PER_BATCH + q;
+      if constexpr (dt < DT) {
+        const uint32_t addr = va ^ (32 * dt);
+        r[2 * q] = lds_read_tr<kAsm, 0>(addr);
+        if constexpr (KSPLIT) r[2 * q + 1] = lds_read_tr<kAsm, 0>(addr ^ (16 * ROWB));
+        else r[2 * q + 1] = lds_read_tr<kAsm, 16 * ROWB>(addr);
       } else {
         r[2 * q] = u32x2{0u, 0u};
         r[2 * q + 1] = u32x2{0u, 0u};
@@ -656,103 +667,108 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // shift is applied once, as a rescale between the exact and the
     // correction walks)
     constexpr bool RAW = kFree && MODE == 0;
-    f32x16(&s_new)[RG] = s_buf[B];
-    f32x16(&s_old)[RG] = s_buf[1 - B];
-    constexpr int KW = KSQ < 4 ? KSQ : 4;  // K fragment reads in flight
-    const uint32_t va = vbase_own + p_pend.off;
-    const uint32_t va2 = vbase_oth + p_pend.off;
+    f32x4(&s_new)[RT][KT] = s_buf[B];
+    f32x4(&s_old)[RT][KT] = s_buf[1 - B];
+    constexpr int KW = KR < 4 ? KR : 4;  // K fragment reads in flight
+    const uint32_t va = vbase + p_pend.off;
     const uint32_t ka = kbase + nw.off;
     u32x2 vb[2][8];
-    u32x4 kf[KSQ];
-    vec8 pb[RG][2];
+    u32x4 kf[KR];
+    vec8 pb[RT];
+    // K fragment read i: k-step i / 2, key tile i % 2 (DS = 2: tile 0 is the
+    // wave's own, 16*dhalf rows in)
+    auto read_k = [&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      constexpr int ks = i / 2, kt = i % 2;
+      if constexpr (KSPLIT) return lds_read_b128<kAsm, 0>(ka ^ (64 * ks + kt * 16 * ROWB));
+      else return lds_read_b128<kAsm, kt * 16 * ROWB>(ka ^ (64 * ks));
+    };
 
     // ---- stage A ----
     // Wave priority: a wave in the VALU-heavy stage A yields issue to the
     // other wave of its SIMD when that one is in stage B (PV MFMAs, light
-    // VALU) or in its fills, which keeps the matrix pipe fed (measured: 4%
-    // on the 128k layer).
+    // VALU) or in its fills, which keeps the matrix pipe fed.
     __builtin_amdgcn_s_setprio(0);
     // A window of KW K fragments of the new slice, then V^T batch 0 of the
-    // pending slice; each QK MFMA issues the read KW fragments ahead.  Reads
-    // complete in order, so fragment i is ready once at most the reads issued
-    // after it are outstanding.  The exp section of the
+    // pending slice; each group of QK MFMAs issues the read KW fragments
+    // ahead.  Reads complete in order, so fragment i is ready once at most
+    // the reads issued after it are outstanding.  The exp section of the
     // pending slice is spread over the QK MFMAs in source order; an empty asm
     // that consumes each piece keeps the compiler from regrouping them.
     if constexpr (HN) {
       StaticFor<0, KW>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        kf[i] = lds_read_b128<kAsm, 0>(ka ^ (32 * i));
+        kf[i] = read_k(ic);
       });
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) s_new[rg] = f32x16{};
+      for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) s_new[rt][kt] = f32x4{};
+      }
     }
     // V^T batch 0 after the first K window: those K reads do not wait behind it
-    if constexpr (HP) issue_v(va, va2, std::integral_constant<int, 0>{}, vb[0]);
+    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
     constexpr int NV0 = HP ? 2 * PER_BATCH : 0;  // reads of batch 0
-    float bias[RG];
+    float bias[RT];
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
-      bias[rg] = 0.f;
+    for (int rt = 0; rt < RT; ++rt) {
+      bias[rt] = 0.f;
       // (the logit shift of correction slices selected as scalar bits, so
       // the add takes it from an SGPR)
       if constexpr (HP && !RAW)
-        bias[rg] = bias_of_ref(rg) +
+        bias[rt] = bias_of_ref(rt) +
                    __uint_as_float(__builtin_amdgcn_readfirstlane(p_pend.corr ? __float_as_uint(a.shift) : 0u));
     }
-    u32x4 w[RG][2];
-    // P for the pair of keys (2pi, 2pi+1) of the pending slice in row group
-    // rg, for the pair number f = pi * RG + rg (the row groups alternate)
+    // P words of the pending slice: w[rt][e] packs keys 2e, 2e + 1 of the
+    // PV contraction slots (slot 4kt + r: key 16kt + 4grp + r).  DS = 2: the
+    // wave computes its own key tile's words (e = 0, 1); the partner's
+    // arrive through LDS as e = 2, 3.
+    u32x4 w[RT];
+    constexpr int NP = KSPLIT ? 2 * RT : 4 * RT;  // exp pairs per slice
     auto exp_pair = [&](auto fc) {
       constexpr int f = decltype(fc)::value;
-      constexpr int rg = f % RG, pi = f / RG;
-      const float x0 = RAW ? s_old[rg][2 * pi] : fmaf(s_old[rg][2 * pi], c_pos, bias[rg]);
-      const float x1 = RAW ? s_old[rg][2 * pi + 1] : fmaf(s_old[rg][2 * pi + 1], c_pos, bias[rg]);
+      constexpr int rt = f / (NP / RT), e = f % (NP / RT);
+      constexpr int kt = e / 2, r0 = 2 * (e % 2);
+      const float x0 = RAW ? s_old[rt][kt][r0] : fmaf(s_old[rt][kt][r0], c_pos, bias[rt]);
+      const float x1 = RAW ? s_old[rt][kt][r0 + 1] : fmaf(s_old[rt][kt][r0 + 1], c_pos, bias[rt]);
       const float p0 = __builtin_amdgcn_exp2f(x0);
       const float p1 = __builtin_amdgcn_exp2f(x1);
       const uint32_t word = pack2<T>(p0, p1);
-      l_run[rg] = add_pair<T>(word, l_run[rg]);  // row sum of the rounded P used below
-      w[rg][pi / 4][pi % 4] = word;
+      l_run[rt] = add_pair<T>(word, l_run[rt]);  // row sum of the rounded P used below
+      w[rt][e] = word;
       asm volatile("" ::"v"(word));
     };
-    // exp pairs per slice (DS = 2: the wave's own 16 keys, S elements 0-7)
-    constexpr int NP = KSPLIT ? 4 : 8 * RG;
     if constexpr (HN) {
-      // kExpLead pairs first, while the first K fragments are in flight,
-      // then the rest spread over the QK MFMAs.
-      constexpr int E0 = HP ? kExpLead * RG : 0;
-      constexpr int EA = KSPLIT ? NP : kExpA * RG;  // (DS = 2: all before the exchange)
-      if constexpr (HP) StaticFor<0, E0>::run(exp_pair);
-      StaticFor<0, KSQ>::run([&](auto ic) {
+      constexpr int EA = KSPLIT ? NP : kExpA;  // (DS = 2: all before the exchange)
+      StaticFor<0, KR>::run([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         // reads issued after K fragment i: the rest of the first window, the
-        // V batch, and the fragments issued by earlier MFMAs of the loop
-        constexpr int LATE = KSQ - KW > 0 ? KSQ - KW : 0;
+        // V batch, and the fragments issued by earlier MFMA groups
+        constexpr int LATE = KR - KW > 0 ? KR - KW : 0;
         constexpr int Y0 = KW - 1 - i + NV0 + (i < LATE ? i : LATE);
         constexpr int younger = i < KW ? (Y0 < 15 ? Y0 : 15)
-                                       : ((KSQ - 1 - i) < (KW - 1) ? (KSQ - 1 - i) : (KW - 1));
+                                       : ((KR - 1 - i) < (KW - 1) ? (KR - 1 - i) : (KW - 1));
         lgkm_wait<kAsm, younger>(kf[i]);
+        constexpr int ks = i / 2, kt = i % 2;
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg) s_new[rg] = Elem<T>::mfma32(as_vec8<T>(kf[i]), qf[rg][i], s_new[rg]);
-        if constexpr (i + KW < KSQ) kf[i + KW] = lds_read_b128<kAsm, 0>(ka ^ (32 * (i + KW)));
-        if constexpr (HP)
-          StaticFor<E0 + i * (EA - E0) / KSQ, E0 + (i + 1) * (EA - E0) / KSQ>::run(exp_pair);
+        for (int rt = 0; rt < RT; ++rt)
+          s_new[rt][kt] = Elem<T>::mfma16(as_vec8<T>(kf[i]), qf[rt][ks], s_new[rt][kt]);
+        if constexpr (i + KW < KR) kf[i + KW] = read_k(std::integral_constant<int, i + KW>{});
+        if constexpr (HP) StaticFor<i * EA / KR, (i + 1) * EA / KR>::run(exp_pair);
       });
     } else if constexpr (HP) {
       StaticFor<0, NP>::run(exp_pair);
     }
-    constexpr int EB = (HN && !KSPLIT) ? kExpA * RG : NP;  // pairs done once stage A ends
-    if constexpr (HP) {
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        pb[rg][0] = as_vec8<T>(w[rg][0]);
-        if constexpr (EB == NP && !KSPLIT) pb[rg][1] = as_vec8<T>(w[rg][1]);
-      }
+    constexpr int EB = (HN && !KSPLIT) ? kExpA : NP;  // pairs done once stage A ends
+    if constexpr (HP && !KSPLIT) {
+      pb[0] = as_vec8<T>(w[0]);
+      if constexpr (EB == NP) pb[1] = as_vec8<T>(w[1]);
     }
 
-    // DS = 2: exchange with the partner wave: the partial S of its keys
-    // (elements 8-15) for the partner's partial of ours, added to elements
-    // 0-7, and the P of the pending slice's own keys for the partner's P,
-    // the second P operand of stage B.  Every wave of the workgroup takes
+    // DS = 2: exchange with the partner wave: the partial S of its key tile
+    // (s[rt][1]) for the partner's partial of ours, added to s[rt][0], and
+    // the P words of the pending slice's own keys for the partner's, the
+    // second half of the PV contraction.  Every wave of the workgroup takes
     // this path in the same calls, so the barriers are uniform.  A wave
     // writes its area only after a barrier that follows the partner's reads
     // of the previous contents: the sub-tile's barrier, or for the call of
@@ -763,39 +779,46 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       if constexpr (!HN) barrier_lds();
       if constexpr (HN) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          reinterpret_cast<f32x4*>(mine + 2048)[j * 64 + lane] =
-              f32x4{s_new[0][8 + 4 * j], s_new[0][9 + 4 * j], s_new[0][10 + 4 * j], s_new[0][11 + 4 * j]};
+        for (int rt = 0; rt < RT; ++rt) reinterpret_cast<f32x4*>(mine + 2048)[rt * 64 + lane] = s_new[rt][1];
       }
-      if constexpr (HP) reinterpret_cast<u32x4*>(mine)[lane] = w[0][0];
+      if constexpr (HP)
+        reinterpret_cast<u32x4*>(mine)[lane] = u32x4{w[0][0], w[0][1], w[1][0], w[1][1]};
       barrier_lds();
       if constexpr (HN) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const f32x4 v = reinterpret_cast<const f32x4*>(theirs + 2048)[j * 64 + lane];
+        for (int rt = 0; rt < RT; ++rt) {
+          const f32x4 v = reinterpret_cast<const f32x4*>(theirs + 2048)[rt * 64 + lane];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s_new[0][4 * j + e] += v[e];
+          for (int e = 0; e < 4; ++e) s_new[rt][0][e] += v[e];
         }
       }
-      if constexpr (HP) pb[0][1] = as_vec8<T>(reinterpret_cast<const u32x4*>(theirs)[lane]);
+      if constexpr (HP) {
+        const u32x4 v = reinterpret_cast<const u32x4*>(theirs)[lane];
+        w[0][2] = v[0];
+        w[0][3] = v[1];
+        w[1][2] = v[2];
+        w[1][3] = v[3];
+        pb[0] = as_vec8<T>(w[0]);
+        pb[1] = as_vec8<T>(w[1]);
+      }
     }
 
     // mask of the new slice (diagonal / partial slices only)
     if constexpr (HN && MASK) {
-      // Element j holds key e = hf*4 + c_j of the slice, c_j = (j/4)*8 + j%4;
-      // it is kept iff e < nkeys and (correction, or e <= qpos - key0), i.e.
-      // iff c_j <= lim with one per-lane limit, so the 16 tests compare
-      // against immediates.
-      // (DS = 2: only elements 0-7, whose keys are 16 higher for the
-      // second wave of a pair)
+      // Element r of s[rt][kt] holds key 16kt + 4grp + r of the slice; it is
+      // kept iff that key is < nkeys and (correction, or <= qpos - key0),
+      // i.e. iff 16kt + r <= lim with one per-lane limit, so the tests
+      // compare against immediates.  (DS = 2: only the own tile, whose keys
+      // are 16*dhalf higher.)
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        int lim = nw.nkeys - 1 - hf * 4 - (KSPLIT ? 16 * dhalf : 0);
-        if (!nw.corr) lim = min(lim, qpos_abs[rg] - nw.key0 - hf * 4 - (KSPLIT ? 16 * dhalf : 0));
+      for (int rt = 0; rt < RT; ++rt) {
+        const int base = 4 * grp + (KSPLIT ? 16 * dhalf : 0);
+        int lim = nw.nkeys - 1 - base;
+        if (!nw.corr) lim = min(lim, qpos_abs[rt] - nw.key0 - base);
 #pragma unroll
-        for (int j = 0; j < (KSPLIT ? 8 : 16); ++j) {
-          const int cj = (j >> 2) * 8 + (j & 3);
-          s_new[rg][j] = cj <= lim ? s_new[rg][j] : neg_inf();
+        for (int kt = 0; kt < (KSPLIT ? 1 : KT); ++kt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s_new[rt][kt][r] = (16 * kt + r) <= lim ? s_new[rt][kt][r] : neg_inf();
         }
       }
     }
@@ -803,89 +826,96 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // ---- stage B ----
     __builtin_amdgcn_s_setprio(1);
     // PV MFMAs of the pending slice with the row max of the new one spread
-    // over them.
-    float mx[RG];
+    // over them.  Each V^T fragment serves both row tiles: per batch, the
+    // first row tile's MFMAs (over which the last exp pairs are spread),
+    // then the second's.
+    float mx[RT];
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) mx[rg] = neg_inf();
-    // max of the key pair (2j, 2j+1) of row group rg, step f = j * RG + rg
+    for (int rt = 0; rt < RT; ++rt) mx[rt] = neg_inf();
+    constexpr int NM = KSPLIT ? 2 * RT : 4 * RT;  // max steps: one v_max3 per key pair
     auto max_step = [&](auto fc) {
       constexpr int f = decltype(fc)::value;
-      constexpr int rg = f % RG, j = f / RG;
-      mx[rg] = fmaxf(fmaxf(mx[rg], s_new[rg][2 * j]), s_new[rg][2 * j + 1]);
-      asm volatile("" : "+v"(mx[rg]));
+      constexpr int rt = f / (NM / RT), e = f % (NM / RT);
+      constexpr int kt = e / 2, r0 = 2 * (e % 2);
+      mx[rt] = fmaxf(fmaxf(mx[rt], s_new[rt][kt][r0]), s_new[rt][kt][r0 + 1]);
+      asm volatile("" : "+v"(mx[rt]));
     };
+    constexpr int PV_OPS = 2 * DT;  // PV MFMAs per slice
     if constexpr (HP) {
       lgkm_wait<kAsm, 0>(vb[0]);
       StaticFor<0, BATCHES>::run([&](auto bc) {
         constexpr int b = decltype(bc)::value;
-        if constexpr (b + 1 < BATCHES) issue_v(va, va2, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
-        StaticFor<0, PER_BATCH>::run([&](auto qc) {
-          constexpr int q = decltype(qc)::value;
-          constexpr int op = b * PER_BATCH + q;
-          if constexpr (op < PV_OPS) {
-            constexpr int u = op / DT, dt = op % DT;
+        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
+        constexpr int NQ = (DT - b * PER_BATCH) < PER_BATCH ? (DT - b * PER_BATCH) : PER_BATCH;
+        StaticFor<0, 2 * PER_BATCH>::run([&](auto qc) {
+          constexpr int j = decltype(qc)::value;
+          constexpr int rt = j / PER_BATCH, q = j % PER_BATCH;
+          if constexpr (q < NQ) {
+            constexpr int dt = b * PER_BATCH + q;
             const u32x2(&r)[8] = vb[b & 1];
             const u32x4 av = {r[2 * q][0], r[2 * q][1], r[2 * q + 1][0], r[2 * q + 1][1]};
-#pragma unroll
-            for (int rg = 0; rg < RG; ++rg) {
-              o[rg][dt] = Elem<T>::mfma32(as_vec8<T>(av), pb[rg][u], o[rg][dt]);
+            o[dt][rt] = Elem<T>::mfma16(as_vec8<T>(av), pb[rt], o[dt][rt]);
+            // the last exp pairs (the second row tile's) over the first
+            // row tile's MFMAs of batch 0
+            if constexpr (EB < NP && b == 0 && rt == 0) {
+              StaticFor<EB + q * (NP - EB) / NQ, EB + (q + 1) * (NP - EB) / NQ>::run(exp_pair);
+              if constexpr (q + 1 == NQ) pb[1] = as_vec8<T>(w[1]);
             }
-            if constexpr (EB < NP && op < DT) {
-              StaticFor<EB + op * (NP - EB) / DT, EB + (op + 1) * (NP - EB) / DT>::run(exp_pair);
-              if constexpr (op + 1 == DT) {
-#pragma unroll
-                for (int rg = 0; rg < RG; ++rg) pb[rg][1] = as_vec8<T>(w[rg][1]);
-              }
-            }
-            // the row max starts kMaxDelay MFMAs in, when S^T has landed
-            constexpr int DM = kMaxDelay < PV_OPS ? kMaxDelay : PV_OPS - 1;
-            if constexpr (MAX && op >= DM)
-              StaticFor<(op - DM) * NP / (PV_OPS - DM), (op - DM + 1) * NP / (PV_OPS - DM)>::run(max_step);
+            // the row max of the new slice, spread over the PV MFMAs (op:
+            // this MFMA's index; every earlier batch is full)
+            constexpr int op = b * 2 * PER_BATCH + rt * NQ + q;
+            if constexpr (MAX) StaticFor<op * NM / PV_OPS, (op + 1) * NM / PV_OPS>::run(max_step);
           }
         });
         if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
       });
+      static_assert(PV_OPS == 2 * (BATCHES - 1) * PER_BATCH + 2 * (DT - (BATCHES - 1) * PER_BATCH),
+                    "only the last batch is partial");
     } else if constexpr (MAX) {
-      StaticFor<0, NP>::run(max_step);
+      StaticFor<0, NM>::run(max_step);
     }
 
     // ---- stage C: reference max of the new slice ----
-    // (DS = 2: the max over the wave's own keys, then over the partner's
-    // through LDS; the partner's previous read of this word was consumed
-    // before the barrier of this sub-tile)
-    auto row_max = [&](int rg) {
-      float m = pair_max(mx[rg]);
+    // (the max over the four lanes of the row; DS = 2: then over the
+    // partner's keys through LDS, whose previous read of this area was
+    // consumed before the barrier of this sub-tile)
+    auto row_max = [&](int rt) { return quad_max(mx[rt]); };
+    float mrow[RT];
+    if constexpr (MAX) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) mrow[rt] = row_max(rt);
       if constexpr (KSPLIT) {
-        reinterpret_cast<float*>(xbuf + wave * 4096 + 1024)[lane] = m;
+        reinterpret_cast<f32x2*>(xbuf + wave * 4096 + 1024)[lane] = f32x2{mrow[0], mrow[1]};
         barrier_lds();
-        m = fmaxf(m, reinterpret_cast<const float*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane]);
+        const f32x2 v = reinterpret_cast<const f32x2*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane];
+        mrow[0] = fmaxf(mrow[0], v[0]);
+        mrow[1] = fmaxf(mrow[1], v[1]);
       }
-      return m;
-    };
+    }
     if constexpr (MAX && MODE == 1) {
       // the first slice: O and l are still zero, no rescale
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        m_ref[rg] = fmaf(row_max(rg), c_pos, nw.corr ? a.shift : 0.f);
-        neg_m[rg] = (m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg];
-        m_thr[rg] = m_ref[rg] + kRescaleSlack;
+      for (int rt = 0; rt < RT; ++rt) {
+        m_ref[rt] = fmaf(mrow[rt], c_pos, nw.corr ? a.shift : 0.f);
+        neg_m[rt] = (m_ref[rt] == neg_inf()) ? 0.f : -m_ref[rt];
+        m_thr[rt] = m_ref[rt] + kRescaleSlack;
       }
     }
     if constexpr (MAX && MODE == 2) {
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        const float m_cand = fmaf(row_max(rg), c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
-        if (__ballot(m_cand > thr_of_ref(rg)) != 0ull) {
-          const float m_new = fmaxf(m_ref[rg], m_cand);
-          const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref[rg] - m_new);
-          m_ref[rg] = m_new;
+      for (int rt = 0; rt < RT; ++rt) {
+        const float m_cand = fmaf(mrow[rt], c_pos, nw.corr ? a.shift : 0.f);  // -inf stays -inf (c_pos > 0)
+        if (__ballot(m_cand > thr_of_ref(rt)) != 0ull) {
+          const float m_new = fmaxf(m_ref[rt], m_cand);
+          const float alpha = (m_new == neg_inf()) ? 1.f : __builtin_amdgcn_exp2f(m_ref[rt] - m_new);
+          m_ref[rt] = m_new;
           if constexpr (kKeepRef) {
-            neg_m[rg] = (m_ref[rg] == neg_inf()) ? 0.f : -m_ref[rg];
-            m_thr[rg] = m_ref[rg] + kRescaleSlack;
+            neg_m[rt] = (m_ref[rt] == neg_inf()) ? 0.f : -m_ref[rt];
+            m_thr[rt] = m_ref[rt] + kRescaleSlack;
           }
-          l_run[rg] *= alpha;
+          l_run[rt] *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) scale_in_place(o[rg][dt], alpha);
+          for (int dt = 0; dt < DT; ++dt) scale_in_place(o[dt][rt], alpha);
         }
       }
     }
@@ -970,18 +1000,21 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // workgroup through the walk again with the online reference and rescale
   // (kernel.py:287-310), where P <= 2^8.  The bound 2^64 keeps O finite for
   // |V| up to about 2^64; the finiteness test covers larger V.
-  // DS = 2: row sums over all keys, the two waves' sums of their own keys
-  // added in either order, so both waves hold the same value.
-  float l_pair = 0.f;
-  auto pair_row_sum = [&]() {
+  // Row sums: the four lanes of a row add their keys' sums (DS = 2: then the
+  // two waves of a pair add theirs, in either order, so both hold the same
+  // value).
+  float l_tot[RT];
+  auto row_sums = [&]() {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) l_tot[rt] = quad_sum(l_run[rt]);
     if constexpr (KSPLIT) {
-      l_pair = pair_sum(l_run[0]);
-      reinterpret_cast<float*>(xbuf + wave * 4096 + 1024)[lane] = l_pair;
+      reinterpret_cast<f32x2*>(xbuf + wave * 4096 + 1024)[lane] = f32x2{l_tot[0], l_tot[1]};
       barrier_lds();
-      l_pair += reinterpret_cast<const float*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane];
+      const f32x2 v = reinterpret_cast<const f32x2*>(xbuf + (wave ^ (WAVES / 2)) * 4096 + 1024)[lane];
+      l_tot[0] += v[0];
+      l_tot[1] += v[1];
     }
   };
-  auto row_sum = [&](int rg) { return KSPLIT ? l_pair : pair_sum(l_run[rg]); };
   if constexpr (kFree && CORR) {
     // exact steps, then the correction steps: in between, every weight so
     // far is scaled by 2^-shift = 1/block_k, which gives the pooled entries,
@@ -993,10 +1026,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     if (n_corr > 0) {
       __syncthreads();  // every wave is done with the ring before it is refilled
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) {
-        l_run[rg] *= a.inv_bk;
+      for (int rt = 0; rt < RT; ++rt) {
+        l_run[rt] *= a.inv_bk;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) scale_in_place(o[rg][dt], a.inv_bk);
+        for (int dt = 0; dt < DT; ++dt) scale_in_place(o[dt][rt], a.inv_bk);
       }
       walk_it = n_sel;
       walk_end = n_steps;
@@ -1005,18 +1038,18 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   } else {
     run_walk(False{});
   }
-  pair_row_sum();
+  row_sums();
   bool bad = false;
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
-    const float l = row_sum(rg);
+  for (int rt = 0; rt < RT; ++rt) {
     bool fin = true;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) fin = fin && __builtin_isfinite(o[rg][dt][j]);
+      for (int j = 0; j < 4; ++j) fin = fin && __builtin_isfinite(o[dt][rt][j]);
     }
-    bad = bad || (row_valid[rg] && !(l >= 0x1p-60f && l <= 0x1p64f && fin));
+    const float l = l_tot[rt];
+    bad = bad || (row_valid[rt] && !(l >= 0x1p-60f && l <= 0x1p64f && fin));
   }
   // Workgroup-wide decision through the last ring stage, which the second
   // walk refills only after its first barrier (the flags are read by then).
@@ -1030,13 +1063,13 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   for (int w = 0; w < WAVES; ++w) redo |= flags[w];
   if (redo) {
 #pragma unroll
-    for (int rg = 0; rg < RG; ++rg) {
+    for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
-      for (int i = 0; i < DT; ++i) o[rg][i] = f32x16{};
-      m_ref[rg] = neg_inf();
-      neg_m[rg] = 0.f;
-      m_thr[rg] = neg_inf();
-      l_run[rg] = 0.f;
+      for (int dt = 0; dt < DT; ++dt) o[dt][rt] = f32x4{};
+      m_ref[rt] = neg_inf();
+      neg_m[rt] = 0.f;
+      m_thr[rt] = neg_inf();
+      l_run[rt] = 0.f;
     }
     p_pend = Slice{0, 0, 0, 0u};
     walk_it = 0;
@@ -1046,26 +1079,23 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     if constexpr (CORR) win_next = load_window(64);
     load_cids(0);
     run_walk(True{});
-    pair_row_sum();
+    row_sums();
   }
 
   // ---- normalise and store ----
+  // O^T tile (dt, rt): the lane holds dims 16dt + 4grp + 0..3 of its row
 #pragma unroll
-  for (int rg = 0; rg < RG; ++rg) {
-    const float l_tot = row_sum(rg);
-    if (!exists[rg] || pos[rg] >= a.out_rows) continue;
-    const float inv = (row_valid[rg] && l_tot > 0.f) ? 1.f / l_tot : 0.f;
-    uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g[rg]) * a.o_hs + pos[rg] * a.o_rs;
+  for (int rt = 0; rt < RT; ++rt) {
+    if (!exists[rt] || pos[rt] >= a.out_rows) continue;
+    const float inv = (row_valid[rt] && l_tot[rt] > 0.f) ? 1.f / l_tot[rt] : 0.f;
+    uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g[rt]) * a.o_hs + pos[rt] * a.o_rs;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int jg = 0; jg < 4; ++jg) {
-        const int d0 = (dhalf * DT + dt) * 32 + jg * 8 + hf * 4;
-        u32x2 wv;
-        wv[0] = pack2<T>(o[rg][dt][jg * 4 + 0] * inv, o[rg][dt][jg * 4 + 1] * inv);
-        wv[1] = pack2<T>(o[rg][dt][jg * 4 + 2] * inv, o[rg][dt][jg * 4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d0) = wv;
-      }
+      const int d0 = (dhalf * DT + dt) * 16 + grp * 4;
+      u32x2 wv;
+      wv[0] = pack2<T>(o[dt][rt][0] * inv, o[dt][rt][1] * inv);
+      wv[1] = pack2<T>(o[dt][rt][2] * inv, o[dt][rt][3] * inv);
+      *reinterpret_cast<u32x2*>(orow + d0) = wv;
     }
   }
 }
