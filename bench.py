@@ -18,7 +18,8 @@ Reported beside it (each a BASELINE config unless labelled otherwise):
 ``alpha_0.05`` / ``alpha_0.2`` (config 3's sweep), ``contrast_variant`` (the
 sparse regime: planted x 3*sqrt(D), most blocks pruned, correction phase
 active; labelled supplementary), ``kv_head_share`` (one GPU's share of the
-primary layer under KV-head sharding: one KV head and its query heads),
+primary layer under KV-head sharding: one KV head and its query heads;
+``kv_head_share_contrast`` on the contrast generator),
 ``chunked_64k`` (config 4; ``chunked_64k_contrast`` on the contrast
 generator), ``other_geometries_32k`` (config 2's layer at head_dim 64, 96,
 256 and in float16), and
@@ -639,6 +640,12 @@ def main(argv=None) -> int:
         share["label"] = ("one GPU's share of the primary layer under KV-head sharding over "
                           f"{HKV} GPUs (Hq {HQ // HKV}, Hkv 1; design only, no collective runs)")
         extra["kv_head_share"] = share
+        torch.cuda.empty_cache()
+        share_c, _ = run_config(torch, args.seq, args.alpha, x_steps, x_warm,
+                                query_heads=HQ // HKV, kv_heads=1, planted=3.0 * math.sqrt(D))
+        share_c["label"] = ("one GPU's share under KV-head sharding, contrast generator: its "
+                            "dense-tail tiles run split by key range")
+        extra["kv_head_share_contrast"] = share_c
         torch.cuda.empty_cache()
         extra["chunked_64k"] = run_chunked(torch, 65536, 2048, args.alpha)
         torch.cuda.empty_cache()

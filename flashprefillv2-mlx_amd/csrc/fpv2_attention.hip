@@ -122,6 +122,15 @@ struct AttnArgs {
   int64_t pooled_hs;  // elements between KV heads of pk / pv
   int q_rs, k_rs, v_rs;
   uint32_t q_bytes, k_bytes, v_bytes, pooled_bytes;  // descriptor ranges
+  // (last, so that the whole-tile kernel reads its other fields at the
+  // offsets it had before the split existed)
+  // Dense-tail split: the last split_tiles tiles run as nseg workgroups
+  // each, over seg_steps consecutive sub-tiles of the tile's walk apiece,
+  // writing unnormalised partials (O, l) and their scale m (the partial is
+  // (O, l) * 2^m in the common scale of exp2(logit)) for merge_split_kernel.
+  int split_tiles, nseg, seg_steps;
+  float* ws_o;    // [item][seg][RW rows][D]
+  float* ws_ml;   // [item][seg][RW rows][2]: m, l
 };
 
 // Workgroup barrier for data written to LDS by ds_write: it waits for this
@@ -182,7 +191,10 @@ struct Step {
 // softmax work is not repeated.  Each accumulates its half of O from both
 // halves of P.  This keeps D = 256 at two waves per SIMD within 256
 // registers.
-template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
+// SEG: the launch of the split tiles' segments (every workgroup is one
+// segment of one split tile), instantiated apart so that the whole-tile
+// kernel's code carries nothing of it.
+template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1, bool SEG = false>
 __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void sparse_attn_kernel(AttnArgs a) {
   using GM = Geom<D>;
   constexpr int RT = 2;  // 16-row query tiles per wave (32 rows)
@@ -220,11 +232,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const int grp = lane >> 4;  // 16-lane group: keys 4*grp.. of each key tile
 
   // ---- workgroup -> (KV head, tile, row chunk); latest tiles first ----
+  // Whole tiles: [0, Nt - split_tiles).  Segments (SEG): seg of the split
+  // tiles [Nt - split_tiles, Nt).  The KV head is in the low bits.
   const int bid = blockIdx.x;
   const int h = bid % a.Hkv;
-  const int rest = bid / a.Hkv;
+  int rest = bid / a.Hkv;
+  const int seg = SEG ? rest % a.nseg : -1;
+  if constexpr (SEG) rest /= a.nseg;
   const int chunk = rest % a.nchunk;
-  const int t = a.Nt - 1 - rest / a.nchunk;
+  const int t = (SEG ? a.Nt : a.Nt - a.split_tiles) - 1 - rest / a.nchunk;
   const int abs_first = a.offset + t * a.tq;
   const int last_local = min((t + 1) * a.tq, a.Lq);
   const int abs_last = a.offset + last_local - 1;
@@ -371,14 +387,28 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   auto load_window = [&](int base) {  // raw entry of step base + lane
     return static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(idr, ((base + lane) / subs) * 4, 0, 0));
   };
-  // the first window's entries come from id_lane (its steps cover at most
-  // the first 64 entries)
-  window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
-  int win_next = CORR ? load_window(64) : 0;
-  // A walk covers steps [walk_it, walk_end): all of them, or (the
-  // reference-free pass with correction) the exact steps, then the
+  // A workgroup walks steps [s_lo, s_hi): all of the tile's, or a
+  // segment's seg_steps of them.
+  const int s_lo = SEG ? min(seg * a.seg_steps, n_steps) : 0;
+  const int s_hi = SEG ? min(s_lo + a.seg_steps, n_steps) : n_steps;
+  // The window holding step s: the first window's entries come from id_lane
+  // (its steps cover at most the first 64 entries), later ones are loaded.
+  int win_next = 0;
+  auto start_windows = [&](int s) {
+    win_base = SEG ? (s / 64) * 64 : 0;
+    if (!SEG || win_base == 0) {
+      window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
+    } else {
+      const int li = (win_base + lane) / subs;  // < li_end when the step is < n_sel
+      window_entry(win_base + lane, win_base + lane < n_sel ? clampi(ids[min(li, Nb - 1)], 0, Nb - 1) : 0);
+    }
+    if constexpr (CORR) win_next = load_window(win_base + 64);
+  };
+  start_windows(s_lo);
+  // A walk covers steps [walk_it, walk_end): the workgroup's, or (the
+  // reference-free pass with correction) its exact steps, then its
   // correction steps.
-  int walk_it = 0, walk_end = n_steps;
+  int walk_it = s_lo, walk_end = s_hi;
   auto next_step = [&]() -> Step {
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
     const int it = walk_it++;
@@ -453,7 +483,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     for (int j = 0; j < NIK; ++j)
       cid[j] = CORR ? static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(pr, fill_row(j, lane) * 4, 0, 0)) : 0;
   };
-  load_cids(0);
+  // (the first correction step of the workgroup's range)
+  load_cids(max(s_lo - n_sel, 0) * BN);
   auto fill_step = [&](const Step& s, int stage) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     // (a lambda returning an LDS pointer would drop the kernel from the host
@@ -1021,8 +1052,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // taken as exp2(S), their relative weight 2^shift (kernel.py:349-351);
     // O / l is unchanged by the common factor.  (A rescale inside the walk
     // would make the compiler move O between register ranges every slice.)
-    walk_end = n_sel;
-    run_walk(False{});
+    // (every segment of a tile with correction steps takes the rescale,
+    // so that their partials share one scale)
+    walk_end = SEG ? min(s_hi, n_sel) : n_sel;
+    if (!SEG || walk_it < walk_end) run_walk(False{});
     if (n_corr > 0) {
       __syncthreads();  // every wave is done with the ring before it is refilled
 #pragma unroll
@@ -1031,9 +1064,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) scale_in_place(o[dt][rt], a.inv_bk);
       }
-      walk_it = n_sel;
-      walk_end = n_steps;
-      run_walk(False{});
+      walk_it = SEG ? max(s_lo, n_sel) : n_sel;
+      walk_end = s_hi;
+      if (!SEG || walk_it < walk_end) run_walk(False{});
     }
   } else {
     run_walk(False{});
@@ -1072,14 +1105,38 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       l_run[rt] = 0.f;
     }
     p_pend = Slice{0, 0, 0, 0u};
-    walk_it = 0;
-    walk_end = n_steps;
-    win_base = 0;
-    window_entry(lane, __builtin_amdgcn_ds_bpermute((lane / subs) * 4, id_lane));
-    if constexpr (CORR) win_next = load_window(64);
-    load_cids(0);
+    walk_it = s_lo;
+    walk_end = s_hi;
+    start_windows(s_lo);
+    load_cids(max(s_lo - n_sel, 0) * BN);
     run_walk(True{});
     row_sums();
+  }
+
+  if constexpr (SEG) {
+    // ---- a segment: unnormalised partials for merge_split_kernel ----
+    // The partial is (O, l) * 2^m in the scale of exp2(logit): m = 0 for the
+    // reference-free pass (log2(block_k) after its correction rescale), the
+    // row's reference otherwise (a row that saw no key in its first slice
+    // walked without one).
+    const int item = (h * a.split_tiles + (t - (a.Nt - a.split_tiles))) * a.nchunk + chunk;
+    const int64_t base = static_cast<int64_t>(item) * a.nseg + seg;
+    float* const wo = a.ws_o + base * RW * D;
+    float* const wml = a.ws_ml + base * RW * 2;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if (!exists[rt]) continue;
+      const int r = rwave * 32 + rt * 16 + l16;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4*>(wo + r * D + (dhalf * DT + dt) * 16 + grp * 4) = o[dt][rt];
+      if (grp == 0 && dhalf == 0) {
+        float m = m_ref[rt] == neg_inf() ? 0.f : m_ref[rt];
+        if (kFree && !redo) m = (CORR && n_corr > 0) ? a.shift : 0.f;
+        *reinterpret_cast<f32x2*>(wml + r * 2) = f32x2{m, l_tot[rt]};
+      }
+    }
+    return;
   }
 
   // ---- normalise and store ----
@@ -1100,15 +1157,90 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   }
 }
 
+// Merge of the split tiles' segments: row r of item (h, tile, chunk) is
+// sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M the largest m_s of the
+// segments with l_s > 0, written as the whole-tile kernel writes it (rows
+// past the valid queries as zeros).  One thread per 4 dims of a row.
+template <int D>
+struct MergeShape {
+  static constexpr int TPR = D / 4;         // threads per row
+  static constexpr int ROWS = 256 / TPR;    // rows per workgroup
+};
+template <typename T, int D, int RW>
+__global__ __launch_bounds__(256) void merge_split_kernel(AttnArgs a) {
+  constexpr int TPR = MergeShape<D>::TPR, ROWS = MergeShape<D>::ROWS;
+  constexpr int WPI = (RW + ROWS - 1) / ROWS;  // workgroups per item
+  if (threadIdx.x >= TPR * ROWS) return;
+  const int item = blockIdx.x / WPI;
+  const int r = (blockIdx.x % WPI) * ROWS + threadIdx.x / TPR;
+  const int d0 = (threadIdx.x % TPR) * 4;
+  if (r >= RW) return;
+  const int chunk = item % a.nchunk;
+  const int ht = item / a.nchunk;
+  const int h = ht / a.split_tiles;
+  const int t = a.Nt - a.split_tiles + ht % a.split_tiles;
+  const int prow = chunk * RW + r;
+  if (prow >= a.G * a.tq) return;
+  const int g = prow / a.tq;
+  const int pos = t * a.tq + (prow - g * a.tq);
+  if (pos >= a.out_rows) return;
+  const int64_t base = static_cast<int64_t>(item) * a.nseg;
+  float mx = neg_inf();
+  for (int s = 0; s < a.nseg; ++s) {
+    const f32x2 ml = *reinterpret_cast<const f32x2*>(a.ws_ml + ((base + s) * RW + r) * 2);
+    if (ml[1] > 0.f) mx = fmaxf(mx, ml[0]);
+  }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+  if (pos < a.Lq && mx != neg_inf()) {
+    for (int s = 0; s < a.nseg; ++s) {
+      const f32x2 ml = *reinterpret_cast<const f32x2*>(a.ws_ml + ((base + s) * RW + r) * 2);
+      if (!(ml[1] > 0.f)) continue;
+      const float w = __builtin_amdgcn_exp2f(ml[0] - mx);
+      const f32x4 o = *reinterpret_cast<const f32x4*>(a.ws_o + ((base + s) * RW + r) * D + d0);
+      acc += o * w;
+      l += ml[1] * w;
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t* orow = a.out + (static_cast<int64_t>(h) * a.G + g) * a.o_hs + static_cast<int64_t>(pos) * a.o_rs;
+  u32x2 wv;
+  wv[0] = pack2<T>(acc[0] * inv, acc[1] * inv);
+  wv[1] = pack2<T>(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2*>(orow + d0) = wv;
+}
+
+template <int WAVES, int DS>
+constexpr int rows_per_wg() { return WAVES / DS * 32; }
+
+// Split calls: the segments' launch, the whole tiles' launch, then the
+// merge, in stream order.
 template <typename T, int D, bool CORR, int WAVES, int NST, int DS = 1>
 int launch_attn(AttnArgs a, hipStream_t stream) {
-  auto kernel = sparse_attn_kernel<T, D, CORR, WAVES, NST, DS>;
-  constexpr int RW = WAVES / DS * 32;
+  constexpr int RW = rows_per_wg<WAVES, DS>();
   a.nchunk = (a.G * a.tq + RW - 1) / RW;
-  const int64_t wgs = static_cast<int64_t>(a.Hkv) * a.Nt * a.nchunk;
-  if (wgs > 0x7fffffffLL) return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
-  hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(wgs)), dim3(WAVES * 64), 0, stream, a);
-  return check_launch("sparse_attention");
+  const int64_t seg_wgs = static_cast<int64_t>(a.Hkv) * a.split_tiles * a.nchunk * a.nseg;
+  const int64_t wgs = static_cast<int64_t>(a.Hkv) * (a.Nt - a.split_tiles) * a.nchunk;
+  if (wgs > 0x7fffffffLL || seg_wgs > 0x7fffffffLL)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention: grid too large");
+  if (seg_wgs > 0) {
+    hipLaunchKernelGGL((sparse_attn_kernel<T, D, CORR, WAVES, NST, DS, true>),
+                       dim3(static_cast<unsigned>(seg_wgs)), dim3(WAVES * 64), 0, stream, a);
+    const int rc = check_launch("sparse_attention (segments)");
+    if (rc) return rc;
+  }
+  if (wgs > 0) {
+    hipLaunchKernelGGL((sparse_attn_kernel<T, D, CORR, WAVES, NST, DS, false>),
+                       dim3(static_cast<unsigned>(wgs)), dim3(WAVES * 64), 0, stream, a);
+    const int rc = check_launch("sparse_attention");
+    if (rc) return rc;
+  }
+  if (seg_wgs == 0) return 0;
+  constexpr int WPI = (RW + MergeShape<D>::ROWS - 1) / MergeShape<D>::ROWS;
+  const int64_t mwgs = static_cast<int64_t>(a.Hkv) * a.split_tiles * a.nchunk * WPI;
+  hipLaunchKernelGGL((merge_split_kernel<T, D, RW>), dim3(static_cast<unsigned>(mwgs)), dim3(256), 0,
+                     stream, a);
+  return check_launch("sparse_attention (merge)");
 }
 
 // Workgroup shape, 32-key sub-tiles in a 4-stage ring.  D <= 128: 4 waves
@@ -1143,13 +1275,15 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }  // namespace
 }  // namespace fpv2
 
-extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v,
-                                     const void* pooled_k, const void* pooled_v,
-                                     const int32_t* selected_ids, const int32_t* selected_counts,
-                                     const int32_t* pruned_ids, const int32_t* pruned_counts,
-                                     void* out, int dtype, const fpv2_attn_params* p,
-                                     void* stream) {
-  using namespace fpv2;
+namespace fpv2 {
+namespace {
+
+// Validation of fpv2_sparse_attention's arguments and the kernel arguments
+// they give; returns 0 or the failure status.
+int attn_args(const void* q, const void* k, const void* v, const void* pooled_k,
+              const void* pooled_v, const int32_t* selected_ids, const int32_t* selected_counts,
+              const int32_t* pruned_ids, const int32_t* pruned_counts, void* out, int dtype,
+              const fpv2_attn_params* p, AttnArgs* out_args) {
   if (!p || !q || !k || !v || !pooled_k || !pooled_v || !selected_ids || !selected_counts ||
       !pruned_ids || !pruned_counts || !out)
     return fail(FPV2_ERR_ARGUMENT, "sparse_attention: null argument");
@@ -1234,8 +1368,100 @@ extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v
   a.k_bytes = static_cast<uint32_t>(k_bytes);
   a.v_bytes = static_cast<uint32_t>(v_bytes);
   a.pooled_bytes = static_cast<uint32_t>(pooled_bytes);
+  *out_args = a;
+  return 0;
+}
+
+int dispatch(const AttnArgs& a, int dtype, const fpv2_attn_params* p, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool corr = p->mean_correction != 0;
   return dtype == FPV2_BF16 ? dispatch_attn<bf16_t>(p->head_dim, corr, a, s)
                             : dispatch_attn<f16_t>(p->head_dim, corr, a, s);
+}
+
+// Segments of the dense-tail split: the longest split tile is the last one,
+// whose walk has at most nvis*subs exact steps (every block that starts at
+// or before its last row) and ceil(Nb / 32) correction steps.
+int64_t split_segments(const fpv2_attn_params* p, int64_t seg_steps) {
+  const int64_t abs_last = p->offset + p->query_length - 1;
+  const int64_t nvis = std::min<int64_t>(p->num_blocks, abs_last / p->block_k + 1);
+  const int64_t subs = (p->block_k + 31) / 32;
+  const int64_t steps = nvis * subs + (p->mean_correction ? (p->num_blocks + 31) / 32 : 0);
+  return (steps + seg_steps - 1) / seg_steps;
+}
+
+constexpr int64_t kSplitRows = 128;  // packed query rows per workgroup, every shape
+
+int64_t split_bytes(const fpv2_attn_params* p, int64_t split_tiles, int64_t seg_steps) {
+  if (split_tiles == 0) return 0;
+  const int64_t G = p->query_heads / p->kv_heads;
+  const int64_t nchunk = (G * p->tile_q + kSplitRows - 1) / kSplitRows;
+  const int64_t items = p->kv_heads * split_tiles * nchunk;
+  return items * split_segments(p, seg_steps) * kSplitRows * (p->head_dim + 2) * 4;
+}
+
+}  // namespace
+}  // namespace fpv2
+
+extern "C" int fpv2_sparse_attention(const void* q, const void* k, const void* v,
+                                     const void* pooled_k, const void* pooled_v,
+                                     const int32_t* selected_ids, const int32_t* selected_counts,
+                                     const int32_t* pruned_ids, const int32_t* pruned_counts,
+                                     void* out, int dtype, const fpv2_attn_params* p,
+                                     void* stream) {
+  using namespace fpv2;
+  AttnArgs a{};
+  const int rc = attn_args(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts, pruned_ids,
+                           pruned_counts, out, dtype, p, &a);
+  if (rc) return rc;
+  return dispatch(a, dtype, p, stream);
+}
+
+extern "C" int64_t fpv2_sparse_attention_split_workspace_bytes(const fpv2_attn_params* p,
+                                                               int64_t split_tiles,
+                                                               int64_t seg_steps) {
+  using namespace fpv2;
+  if (!p || p->tile_q <= 0 || p->padded_query_length <= 0 || p->kv_heads <= 0 ||
+      p->query_heads % p->kv_heads || p->block_k <= 0 || p->num_blocks <= 0 ||
+      p->query_length <= 0)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention_split: invalid parameters");
+  if (split_tiles < 0 || split_tiles > p->padded_query_length / p->tile_q || seg_steps < 1)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention_split: split_tiles must lie in [0, num_tiles] and seg_steps be positive");
+  return split_bytes(p, split_tiles, seg_steps);
+}
+
+extern "C" int fpv2_sparse_attention_split(const void* q, const void* k, const void* v,
+                                           const void* pooled_k, const void* pooled_v,
+                                           const int32_t* selected_ids,
+                                           const int32_t* selected_counts,
+                                           const int32_t* pruned_ids, const int32_t* pruned_counts,
+                                           void* out, int dtype, const fpv2_attn_params* p,
+                                           int64_t split_tiles, int64_t seg_steps,
+                                           void* workspace, int64_t workspace_bytes,
+                                           void* stream) {
+  using namespace fpv2;
+  AttnArgs a{};
+  const int rc = attn_args(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts, pruned_ids,
+                           pruned_counts, out, dtype, p, &a);
+  if (rc) return rc;
+  const int64_t need = fpv2_sparse_attention_split_workspace_bytes(p, split_tiles, seg_steps);
+  if (need < 0) return static_cast<int>(need);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention_split: workspace of %lld bytes needed",
+                static_cast<long long>(need));
+  if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 16)
+    return fail(FPV2_ERR_ARGUMENT, "sparse_attention_split: workspace must be 16-byte aligned");
+  const int64_t nseg = split_segments(p, seg_steps);
+  if (split_tiles * nseg * p->kv_heads > 0x7fffffffLL || seg_steps > 0x7fffffffLL)
+    return fail(FPV2_ERR_UNSUPPORTED, "sparse_attention_split: too many segments");
+  if (need > 0) {
+    a.split_tiles = static_cast<int>(split_tiles);
+    a.nseg = static_cast<int>(nseg);
+    a.seg_steps = static_cast<int>(seg_steps);
+    const int64_t G = p->query_heads / p->kv_heads;
+    const int64_t items = p->kv_heads * split_tiles * ((G * p->tile_q + kSplitRows - 1) / kSplitRows);
+    a.ws_o = static_cast<float*>(workspace);
+    a.ws_ml = a.ws_o + items * nseg * kSplitRows * p->head_dim;
+  }
+  return dispatch(a, dtype, p, stream);
 }

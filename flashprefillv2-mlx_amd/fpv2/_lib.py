@@ -17,7 +17,7 @@ import torch
 LIB_NAME = "libfpv2_hip.so"
 # The in-tree build; FPV2_LIBRARY may point at another build of the same ABI.
 LIB_PATH = Path(os.environ.get("FPV2_LIBRARY") or Path(__file__).resolve().parent / LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FPV2_OK = 0
 FPV2_ERR_ARGUMENT = -1
@@ -37,6 +37,8 @@ EXPORTED_SYMBOLS = (
     "fpv2_score_select",
     "fpv2_compact_block_indices",
     "fpv2_sparse_attention",
+    "fpv2_sparse_attention_split_workspace_bytes",
+    "fpv2_sparse_attention_split",
     # decoder-layer operations of the end-to-end harness (fpv2_decoder.h)
     "fpv2_add_rms_norm",
     "fpv2_qk_norm_rope",
@@ -120,6 +122,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fpv2_sparse_attention.restype = ctypes.c_int
     lib.fpv2_sparse_attention.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32,
                                           ctypes.POINTER(AttnParams), vp]
+    lib.fpv2_sparse_attention_split_workspace_bytes.restype = i64
+    lib.fpv2_sparse_attention_split_workspace_bytes.argtypes = [ctypes.POINTER(AttnParams),
+                                                                i64, i64]
+    lib.fpv2_sparse_attention_split.restype = ctypes.c_int
+    lib.fpv2_sparse_attention_split.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32,
+                                                ctypes.POINTER(AttnParams), i64, i64, vp, i64,
+                                                vp]
     f32 = ctypes.c_float
     lib.fpv2_add_rms_norm.restype = ctypes.c_int
     lib.fpv2_add_rms_norm.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]

@@ -249,15 +249,23 @@ def _pooled_ready(pooled_k: torch.Tensor, pooled_v: torch.Tensor):
     return pooled_k, pooled_v
 
 
+# Sub-tiles (32 keys each) per segment of a split tile: 4096 keys, about
+# the walk of a typical tile of a sparse long-context layer.
+SPLIT_SEG_STEPS = 128
+
+
 def _launch_attention(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts,
                       pruned_ids, pruned_counts, out, *, device, scale, config, offset,
                       query_length, key_length, num_blocks, padded_query_length,
-                      out_rows) -> None:
+                      out_rows, split_tiles=0, seg_steps=SPLIT_SEG_STEPS) -> None:
     """Enqueue ``fpv2_sparse_attention`` on the current stream.
 
     ``q``/``k``/``v``/``out`` are ``[H, L, D]`` views (any head and row
     strides with a contiguous last dimension); rows past the valid lengths
-    are never read.
+    are never read.  ``split_tiles``: run the last ``split_tiles`` query
+    tiles as key-range segments of ``seg_steps`` sub-tiles, merged after the
+    kernel (``fpv2_sparse_attention_split``), with a workspace from the
+    caching allocator.
     """
     lib = _lib.load()
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -276,10 +284,23 @@ def _launch_attention(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts
         o_head_stride=out.stride(0), o_row_stride=out.stride(1),
         pooled_head_stride=pooled_k.stride(0))
     with torch.cuda.device(device):
-        status = lib.fpv2_sparse_attention(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), pooled_k.data_ptr(),
-            pooled_v.data_ptr(), ids.data_ptr(), counts.data_ptr(), pids.data_ptr(),
-            pcounts.data_ptr(), out.data_ptr(), _lib.dtype_code(q.dtype), params,
-            _lib.stream_ptr(device))
+        if split_tiles:
+            need = lib.fpv2_sparse_attention_split_workspace_bytes(params, split_tiles,
+                                                                   seg_steps)
+            if need < 0:
+                _lib.check(int(need), "sparse_attention_split")
+            workspace = torch.empty(max(int(need), 1), dtype=torch.uint8, device=device)
+            status = lib.fpv2_sparse_attention_split(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), pooled_k.data_ptr(),
+                pooled_v.data_ptr(), ids.data_ptr(), counts.data_ptr(), pids.data_ptr(),
+                pcounts.data_ptr(), out.data_ptr(), _lib.dtype_code(q.dtype), params,
+                split_tiles, seg_steps, workspace.data_ptr(), int(need),
+                _lib.stream_ptr(device))
+        else:
+            status = lib.fpv2_sparse_attention(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), pooled_k.data_ptr(),
+                pooled_v.data_ptr(), ids.data_ptr(), counts.data_ptr(), pids.data_ptr(),
+                pcounts.data_ptr(), out.data_ptr(), _lib.dtype_code(q.dtype), params,
+                _lib.stream_ptr(device))
     _lib.check(status, "sparse_attention")
 

@@ -34,7 +34,7 @@ import torch
 import torch.nn.functional as F
 
 from fpv2 import _lib
-from fpv2.kernel import SUPPORTED_HEAD_DIMS, _kernel_ready, _launch_attention
+from fpv2.kernel import SPLIT_SEG_STEPS, SUPPORTED_HEAD_DIMS, _kernel_ready, _launch_attention
 from fpv2.selection import FPV2Config, _select_params
 
 try:  # torch >= 2.3
@@ -264,14 +264,43 @@ def _pool_into(lib, k3, v3, pooled_k, pooled_v, *, dtype, valid_rows, num_blocks
         _lib.check(status, "pool_blocks")
 
 
+# Whole-tile workgroups of a call from which on the dense tail is not split:
+# the launch is long enough to absorb the tail's walk (16 per workgroup slot
+# of the chip); measured on the 128k layer (32768 workgroups), splitting
+# gains nothing there and costs a launch.
+SPLIT_MAX_WORKGROUPS = 8192
+
+
+def _dense_tail_split(geo: _Geometry) -> int:
+    """Query tiles of the call to split by key range: the dense tail (the
+    last ``last_n_blocks`` tiles select every visible block,
+    ``selection.py:191-195``) when its walk spans more than two segments and
+    the call has few enough tiles that the tail, which otherwise walks the
+    whole key range in one workgroup per tile, can be its critical path
+    (chunked prefill, one GPU's share of a sharded layer)."""
+    config = geo.config
+    tail = min(config.last_n_blocks, geo.num_tiles)
+    if not tail:
+        return 0
+    rows = geo.query_heads // geo.kv_heads * config.tile_q
+    workgroups = geo.kv_heads * geo.num_tiles * -(-rows // 128)
+    if workgroups >= SPLIT_MAX_WORKGROUPS:
+        return 0
+    last_row = geo.offset + geo.query_length - 1
+    visible = min(geo.num_blocks, last_row // config.block_k + 1)
+    steps = visible * -(-config.block_k // 32)
+    return tail if steps > 2 * SPLIT_SEG_STEPS else 0
+
+
 def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out=None,
-                   marks=None, keep=None, hook_stats=True):
+                   marks=None, keep=None, hook_stats=True, split=None):
     """Selection and block-sparse attention of one hook call, given the
     pooled K/V (``[Hkv, >=Nb, D]`` views sharing one head stride).  Writes
     ``out`` (``[Hq, Lq, D]``, allocated when None) and returns it.
     ``hook_stats``: count the call in the hook's ``block_sparsity`` while
     statistics are on (``patch.py:150-155``); callers with counters of
-    their own pass False."""
+    their own pass False.  ``split``: tiles to split by key range (None: the
+    dense tail when it is long, ``_dense_tail_split``)."""
     config = geo.config
     device = q3.device
     lib = _lib.load()
@@ -307,20 +336,22 @@ def _select_attend(q3, k3, v3, pooled_k, pooled_v, geo: _Geometry, *, scale, out
                           dtype=q3.dtype, device=device)
     if marks is not None:
         marks("attention")
+    split_tiles = _dense_tail_split(geo) if split is None else split
     _launch_attention(
         q3, k3, v3, pooled_k, pooled_v, ids, counts, pruned_ids, pruned_counts, out,
         device=device, scale=scale, config=config, offset=geo.offset,
         query_length=geo.query_length, key_length=geo.key_length, num_blocks=num_blocks,
-        padded_query_length=geo.padded_query_length, out_rows=geo.query_length)
+        padded_query_length=geo.padded_query_length, out_rows=geo.query_length,
+        split_tiles=split_tiles)
     if marks is not None:
         marks("done")
     if keep is not None:
         keep.update(config=config, offset=geo.offset, pooled_k=pooled_k, pooled_v=pooled_v,
-                    lists=(ids, counts, pruned_ids, pruned_counts))
+                    lists=(ids, counts, pruned_ids, pruned_counts), split_tiles=split_tiles)
     return out
 
 
-def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
+def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None, split=None):
     """``fpv2_sdpa`` body.  ``marks(name)`` (optional) is called on the host
     between the launches ("pool", "select", "attention", "done") so a caller
     can record stream events around each kernel; ``keep`` (optional dict)
@@ -341,7 +372,7 @@ def _fpv2_sdpa(q, k, v, *, scale, config, marks=None, keep=None):
     out = torch.empty((1, geo.query_heads, geo.query_length, geo.head_dim), dtype=q.dtype,
                       device=device)
     _select_attend(q3, k3, v3, pooled_k, pooled_v, geo, scale=scale, out=out[0],
-                   marks=marks, keep=keep)
+                   marks=marks, keep=keep, split=split)
     return out
 
 

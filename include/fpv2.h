@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define FPV2_ABI_VERSION 2
+#define FPV2_ABI_VERSION 3
 
 typedef enum fpv2_status {
   FPV2_OK = 0,
@@ -177,6 +177,45 @@ int fpv2_sparse_attention(const void* q, const void* k, const void* v,
                           const int32_t* pruned_ids,
                           const int32_t* pruned_counts, void* out, int dtype,
                           const fpv2_attn_params* params, void* stream);
+
+/*
+ * Workspace bytes fpv2_sparse_attention_split needs (0 when split_tiles is
+ * 0), or a negative fpv2_status.  The segments of a split tile cover
+ * seg_steps 32-key sub-tiles each, counted over the longest walk a split
+ * tile can have: every block that starts at or before the last query row,
+ * plus ceil(Nb / 32) correction sub-tiles with mean_correction.
+ * Workspace: [Hkv * split_tiles * ceil(G * tile_q / 128)] items x segments
+ * x 128 rows of (D float32 partial outputs, then (m, l) float32 pairs).
+ * No counterpart in the reference: its kernel runs a query tile in one
+ * threadgroup (fpv2/kernel.py:248-325).
+ */
+int64_t fpv2_sparse_attention_split_workspace_bytes(const fpv2_attn_params* params,
+                                                    int64_t split_tiles,
+                                                    int64_t seg_steps);
+
+/*
+ * fpv2_sparse_attention with the last split_tiles query tiles of the call
+ * split by key range: each runs as consecutive segments of seg_steps
+ * sub-tiles of its walk in separate workgroups, whose unnormalised partials
+ * (O, row sum, scale) a second kernel merges into out.  Meant for the dense
+ * tail (the last last_n_blocks tiles select every visible block,
+ * fpv2/selection.py:191-195), which otherwise walks the whole key range in
+ * one workgroup.  The result equals fpv2_sparse_attention's up to float32
+ * summation order.  workspace: at least
+ * fpv2_sparse_attention_split_workspace_bytes bytes, 16-byte aligned, owned
+ * by the caller (no contents are kept between calls); calls that share a
+ * workspace on different streams race.  No counterpart in the reference
+ * (see above).
+ */
+int fpv2_sparse_attention_split(const void* q, const void* k, const void* v,
+                                const void* pooled_k, const void* pooled_v,
+                                const int32_t* selected_ids,
+                                const int32_t* selected_counts,
+                                const int32_t* pruned_ids,
+                                const int32_t* pruned_counts, void* out, int dtype,
+                                const fpv2_attn_params* params, int64_t split_tiles,
+                                int64_t seg_steps, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

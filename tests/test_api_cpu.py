@@ -232,7 +232,7 @@ def test_block_sparsity_starts_at_zero():
 
 def _declared_symbols() -> set[str]:
     text = "\n".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
-    return set(re.findall(r"^\s*(?:int|const char\*)\s+(fpv2_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(fpv2_\w+)\s*\(", text, re.M))
 
 
 def test_header_declares_the_bound_symbols():
