@@ -31,6 +31,7 @@
 //   * grid order puts the KV head in the low bits of the workgroup id, so the
 //     round-robin dispatch over the 8 XCDs keeps one head per XCD L2 (for
 //     Hkv = 8), and tiles run latest (longest) first.
+#include <mutex>
 #include <type_traits>
 
 #include "fpv2_common.h"
@@ -1464,4 +1465,67 @@ extern "C" int fpv2_sparse_attention_split(const void* q, const void* k, const v
     a.ws_ml = a.ws_o + items * nseg * kSplitRows * p->head_dim;
   }
   return dispatch(a, dtype, p, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of fpv2_sparse_attention_split: the split's
+// partials live in a file-scope device array, one copy per GPU, held until
+// the process ends.  Its device address is taken once per device (with that
+// device current) by hipGetSymbolAddress; host code never uses the array's
+// name as an address.
+namespace fpv2 {
+namespace {
+
+constexpr int64_t kScratchBytes = int64_t(64) << 20;  // FPV2_SPLIT_SCRATCH_BYTES
+static_assert(kScratchBytes == FPV2_SPLIT_SCRATCH_BYTES, "header and source agree");
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of the scratch array (set up on its first call).
+int scratch_for_current_device(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FPV2_ERR_LAUNCH, "split_static: hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FPV2_ERR_UNSUPPORTED, "split_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(FPV2_ERR_LAUNCH, "split_static: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace fpv2
+
+extern "C" int fpv2_sparse_attention_split_static(const void* q, const void* k, const void* v,
+                                                  const void* pooled_k, const void* pooled_v,
+                                                  const int32_t* selected_ids,
+                                                  const int32_t* selected_counts,
+                                                  const int32_t* pruned_ids,
+                                                  const int32_t* pruned_counts, void* out,
+                                                  int dtype, const fpv2_attn_params* p,
+                                                  int64_t split_tiles, int64_t seg_steps,
+                                                  void* stream) {
+  using namespace fpv2;
+  const int64_t need = fpv2_sparse_attention_split_workspace_bytes(p, split_tiles, seg_steps);
+  if (need < 0) return static_cast<int>(need);
+  if (need > kScratchBytes)
+    return fail(FPV2_ERR_UNSUPPORTED,
+                "sparse_attention_split_static: the split needs %lld bytes of scratch; at most %lld",
+                static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+  }
+  return fpv2_sparse_attention_split(q, k, v, pooled_k, pooled_v, selected_ids, selected_counts,
+                                     pruned_ids, pruned_counts, out, dtype, p, split_tiles,
+                                     seg_steps, ws, need, stream);
 }

@@ -26,6 +26,7 @@ FPV2_ERR_LAUNCH = -3
 
 F32, F16, BF16 = 0, 1, 2
 MAX_BLOCKS = 8192
+SPLIT_SCRATCH_BYTES = 64 << 20  # FPV2_SPLIT_SCRATCH_BYTES
 
 _DTYPE_CODES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -39,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "fpv2_sparse_attention",
     "fpv2_sparse_attention_split_workspace_bytes",
     "fpv2_sparse_attention_split",
+    "fpv2_sparse_attention_split_static",
     # decoder-layer operations of the end-to-end harness (fpv2_decoder.h)
     "fpv2_add_rms_norm",
     "fpv2_qk_norm_rope",
@@ -129,6 +131,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.fpv2_sparse_attention_split.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, i32,
                                                 ctypes.POINTER(AttnParams), i64, i64, vp, i64,
                                                 vp]
+    lib.fpv2_sparse_attention_split_static.restype = ctypes.c_int
+    lib.fpv2_sparse_attention_split_static.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                       i32, ctypes.POINTER(AttnParams), i64, i64,
+                                                       vp]
     f32 = ctypes.c_float
     lib.fpv2_add_rms_norm.restype = ctypes.c_int
     lib.fpv2_add_rms_norm.argtypes = [vp, vp, vp, vp, i32, i64, i64, i64, i64, i64, f32, vp]

@@ -217,6 +217,32 @@ int fpv2_sparse_attention_split(const void* q, const void* k, const void* v,
                                 int64_t seg_steps, void* workspace,
                                 int64_t workspace_bytes, void* stream);
 
+/* Size of the device scratch array of fpv2_sparse_attention_split_static. */
+#define FPV2_SPLIT_SCRATCH_BYTES (64LL << 20)
+
+/*
+ * fpv2_sparse_attention_split without a workspace argument and without any
+ * allocation: the partials live in a file-scope device array of
+ * FPV2_SPLIT_SCRATCH_BYTES, one copy per GPU, kept until the process ends
+ * (its address is taken once per device, on the first call with that
+ * device current).  A split needing more scratch than that
+ * (fpv2_sparse_attention_split_workspace_bytes) fails with
+ * FPV2_ERR_UNSUPPORTED before any launch.  Every partial the merge reads is
+ * written by the same call, so nothing needs clearing; but all calls on one
+ * GPU share the array, so calls that overlap on one GPU (other streams,
+ * other threads) race.  No counterpart in the reference; it is for callers
+ * that cannot allocate device memory (code under graph capture, serving
+ * loops with a fixed memory plan).
+ */
+int fpv2_sparse_attention_split_static(const void* q, const void* k, const void* v,
+                                       const void* pooled_k, const void* pooled_v,
+                                       const int32_t* selected_ids,
+                                       const int32_t* selected_counts,
+                                       const int32_t* pruned_ids,
+                                       const int32_t* pruned_counts, void* out, int dtype,
+                                       const fpv2_attn_params* params, int64_t split_tiles,
+                                       int64_t seg_steps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
