@@ -229,3 +229,95 @@ def test_random_hook_call_matches_oracle(cuda, c):
         # accounting: the device's selected count equals the oracle's
         visible = orc.causal_block_count(hkv, lq, plan["offset"], plan["config"])
         assert sparsity == 1.0 - int(plan["lists"][1].sum()) / visible
+
+
+# ---------------------------------------------------------------------------
+# The fused selection path (``fpv2_score_select`` with lists requested and no
+# score output, positive scale: the hook's call, ``fpv2/patch.py``
+# ``_select_attend``).  It runs the persistent streaming kernel for D <= 128
+# and the owner kernel for D = 256; the cases above reach the mask-only
+# kernels.  Large GQA groups (short tiles), block sizes off the 32-key grid,
+# several 128-row passes per tile and Q views whose row stride is not a
+# whole number of rows (the unswizzled Q fill) are covered here.
+# ---------------------------------------------------------------------------
+
+STREAM_CASES = [
+    dict(case=200 + i, head_dim=d, dtype=dt, kv_heads=hkv, query_heads=hkv * g, block_k=bk,
+         tile_q=tq, alpha=a, sink=bk, window=2 * bk, last_n=ln, corr=True, offset=off, qlen=ql,
+         sign=1.0, seed=31 + i, pad=pad)
+    for i, (d, dt, hkv, g, bk, tq, a, ln, off, ql, pad) in enumerate([
+        (128, torch.bfloat16, 1, 16, 128, 8, 0.1, 1, 0, 600, 0),
+        (128, torch.bfloat16, 1, 32, 64, 4, 0.15, 0, 130, 500, 0),
+        (64, torch.bfloat16, 2, 16, 48, 8, 0.1, 1, 0, 700, 8),
+        (128, torch.float16, 2, 8, 96, 16, 0.05, 2, 77, 650, 8),
+        (64, torch.bfloat16, 1, 32, 256, 4, 0.1, 1, 0, 1100, 0),
+        (128, torch.bfloat16, 2, 4, 16, 32, 0.2, 0, 300, 400, 24),
+        (96, torch.bfloat16, 1, 8, 32, 16, 0.1, 1, 0, 500, 0),
+        (128, torch.bfloat16, 1, 8, 128, 64, 0.1, 1, 64, 900, 8),
+        (256, torch.bfloat16, 1, 16, 48, 8, 0.1, 1, 0, 600, 8),
+    ])]
+
+
+@pytest.mark.parametrize("c", STREAM_CASES, ids=[_id(c) + f"-pad{c['pad']}" for c in STREAM_CASES])
+def test_fused_selection_lists_match_oracle(cuda, c):
+    from fpv2 import _lib
+    from fpv2.selection import _select_params
+
+    d, dtype, bk, tq = c["head_dim"], c["dtype"], c["block_k"], c["tile_q"]
+    hq, hkv, offset, qlen = c["query_heads"], c["kv_heads"], c["offset"], c["qlen"]
+    config = FPV2Config(block_k=bk, tile_q=tq, alpha=c["alpha"], sink_tokens=c["sink"],
+                        window_tokens=c["window"], last_n_blocks=c["last_n"],
+                        mean_correction=c["corr"])
+    ocfg = orc.OracleConfig(**{f: getattr(config, f) for f in orc.OracleConfig.__dataclass_fields__})
+    scale = d ** -0.5
+    lk = offset + qlen
+    q, k, _ = structured_qkv(length=lk, query_heads=hq, kv_heads=hkv, head_dim=d, block_size=bk,
+                             seed=c["seed"], dtype=dtype)
+    lq_pad = -(-qlen // tq) * tq
+    nb = -(-(offset + lq_pad) // bk)
+    # queries in a buffer whose rows carry `pad` extra elements: a strided view
+    qbuf = torch.zeros((hq, lq_pad, d + c["pad"]), dtype=dtype)
+    qbuf[:, :qlen, :d] = q[:, offset:]
+    kp = torch.zeros((hkv, nb * bk, d), dtype=dtype)
+    kp[:, :lk] = k
+    qd = qbuf.to(cuda)[..., :d]
+    assert qd.stride(1) == d + c["pad"]
+    pk = pool_blocks(kp.to(cuda), bk)
+
+    ids = torch.empty((hkv, lq_pad // tq, nb), dtype=torch.int32, device=cuda)
+    pids = torch.empty_like(ids)
+    counts = torch.empty((hkv, lq_pad // tq), dtype=torch.int32, device=cuda)
+    pcounts = torch.empty_like(counts)
+    lib = _lib.load()
+    params = _select_params(qd, nb, kv_heads=hkv, scale=scale, config=config, offset=offset,
+                            query_length=qlen, padded_length=lq_pad, key_length=lk)
+    with torch.cuda.device(cuda):
+        status = lib.fpv2_score_select(qd.data_ptr(), pk.data_ptr(), _lib.dtype_code(dtype),
+                                       params, None, None, ids.data_ptr(), counts.data_ptr(),
+                                       pids.data_ptr(), pcounts.data_ptr(), _lib.stream_ptr(cuda))
+    _lib.check(status, "score_select")
+    torch.cuda.synchronize()
+    ids_n, counts_n, pids_n, pcounts_n = (to_np(x) for x in (ids, counts, pids, pcounts))
+
+    qn = to_np(qbuf)[..., :d]
+    sel_o, _, ratio = orc.block_scores_and_select(qn, to_np(pk), scale=scale, config=ocfg,
+                                                  offset=offset, query_length=qlen,
+                                                  return_ratio=True)
+    dev_sel = np.zeros(sel_o.shape, dtype=bool)
+    for h in range(hkv):
+        for t in range(ids_n.shape[1]):
+            dev_sel[h, t, ids_n[h, t, :counts_n[h, t]]] = True
+    differ = (dev_sel != sel_o) & ~(np.abs(ratio - config.alpha) <= BAND)
+    assert not differ.any(), f"{int(differ.sum())} block decisions differ outside the band"
+    # the lists are the oracle's compaction of the device's decisions, bit for bit
+    o_ids, o_counts, o_pids, o_pcounts = orc.compact_block_indices(
+        dev_sel, config=ocfg, offset=offset, query_length=qlen, key_length=lk)
+    assert np.array_equal(ids_n, o_ids) and np.array_equal(counts_n, o_counts)
+    assert np.array_equal(pcounts_n, o_pcounts)
+    head = np.arange(nb)[None, None, :] < o_pcounts[..., None]
+    assert np.array_equal(np.where(head, pids_n, -1), np.where(head, o_pids, -1))
+    # and the mask-only kernel decides the same blocks outside the band
+    sel_m, _ = block_scores_and_select(qd, pk, scale=scale, config=config, offset=offset,
+                                       query_length=qlen)
+    differ_m = (to_np(sel_m) != dev_sel) & ~(np.abs(ratio - config.alpha) <= BAND)
+    assert not differ_m.any()
