@@ -899,6 +899,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
             if constexpr (MAX) StaticFor<op * NM / PV_OPS, (op + 1) * NM / PV_OPS>::run(max_step);
           }
         });
+        // the batch's MFMAs stay ahead of the wait for the next batch's
+        // reads (otherwise the scheduler sinks them past it and the matrix
+        // pipe idles while the reads land)
+        __builtin_amdgcn_sched_barrier(0);
         if constexpr (b + 1 < BATCHES) lgkm_wait<kAsm, 0>(vb[(b + 1) & 1]);
       });
       static_assert(PV_OPS == 2 * (BATCHES - 1) * PER_BATCH + 2 * (DT - (BATCHES - 1) * PER_BATCH),
