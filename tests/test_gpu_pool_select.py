@@ -50,6 +50,34 @@ def test_pool_blocks_bit_exact(cuda, dtype, head_dim):
     assert np.array_equal(to_np(got), want)
 
 
+@pytest.mark.parametrize(("head_dim", "block"), [(8, 128), (16, 48), (32, 16), (512, 128), (520, 64), (256, 200)])
+def test_pool_lane_layouts(cuda, head_dim, block):
+    """Head dims and block sizes across the 16-byte kernel's lane layouts
+    (R = 8 row groups per wave with 1, 2 or 4 of 8 padded columns in use;
+    R = 1 at D = 512), the generic kernel past D = 512, and blocks that are
+    not a multiple of the row-group count: whole blocks (``pool_blocks``) and
+    a partial last block (``fpv2_pool_kv``, missing rows counted as zeros)."""
+    gen = torch.Generator().manual_seed(head_dim + block)
+    x = (torch.randn((2, 3 * block, head_dim), generator=gen) * 3.0).bfloat16()
+    got = pool_blocks(x.to(cuda), block)
+    assert got.shape == (2, 3, head_dim)
+    assert np.array_equal(to_np(got), orc.pool_blocks(to_np(x), block, out_dtype="bf16"))
+    valid = 3 * block - 5
+    kd = x.to(cuda)
+    vd = (x * -0.5).to(cuda)
+    pk = torch.empty((2, 3, head_dim), dtype=torch.bfloat16, device=cuda)
+    pv = torch.empty_like(pk)
+    lib = _lib.load()
+    status = lib.fpv2_pool_kv(kd.data_ptr(), vd.data_ptr(), pk.data_ptr(), pv.data_ptr(),
+                              _lib.BF16, 2, valid, 3, head_dim, block, kd.stride(0), kd.stride(1),
+                              pk.stride(0), _lib.stream_ptr(cuda))
+    _lib.check(status, "pool_kv")
+    for src, pooled in ((kd, pk), (vd, pv)):
+        pad = to_np(src).copy()
+        pad[:, valid:] = 0.0
+        assert np.array_equal(to_np(pooled), orc.pool_blocks(pad, block, out_dtype="bf16"))
+
+
 def test_pool_blocks_leading_dims_and_strided_input(cuda):
     x = torch.randn((2, 3, 384, 64), generator=torch.Generator().manual_seed(1)).bfloat16()
     xs = x.to(cuda).transpose(1, 2).contiguous().transpose(1, 2)  # head-strided view
