@@ -410,10 +410,16 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // reference-free pass with correction) its exact steps, then its
   // correction steps.
   int walk_it = s_lo, walk_end = s_hi;
-  auto next_step = [&]() -> Step {
+  // KIND: 0 a walk of both kinds of steps, 1 of exact steps only, 2 of
+  // correction steps only.  (A walk of correction steps has no window to
+  // carry: where one walk served both, the compiler waited for the window
+  // load with vmcnt(0) before copying its register at every correction
+  // step, which drained the fills in flight.)
+  auto next_step = [&](auto kind_c) -> Step {
+    constexpr int KIND = decltype(kind_c)::value;
     Step s{0, 0, 0, 0};  // past the end: an empty sub-tile (all-zero fill)
     const int it = walk_it++;
-    if (it < n_sel && it < walk_end) {
+    if (KIND != 2 && it < n_sel && it < walk_end) {
       if (it - win_base >= 64) {
         win_base += 64;
         if constexpr (CORR) {
@@ -426,7 +432,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
       s.key0 = __builtin_amdgcn_readlane(win_key0, it - win_base);
       s.nkeys = __builtin_amdgcn_readlane(win_nk, it - win_base);
-    } else if (it < walk_end) {
+    } else if (KIND != 1 && it < walk_end) {
       s.corr = 1;
       s.li = (it - n_sel) * BN;
       s.nkeys = min(pr_count - s.li, BN);
@@ -976,7 +982,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   using False = std::integral_constant<bool, false>;
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  auto run_walk = [&](auto online_c) {
+  auto run_walk = [&](auto online_c, auto kind_c) {
     constexpr bool ONLINE = decltype(online_c)::value;
     // (the reference-free pass computes no row max, not even for the first slice)
     using MFirst = std::integral_constant<int, ONLINE ? 2 : (kFree ? 0 : 1)>;
@@ -985,7 +991,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     Step pend[LA];
 #pragma unroll
     for (int p = 0; p < LA; ++p) {
-      pend[p] = next_step();
+      pend[p] = next_step(kind_c);
       fill_step(pend[p], p);
     }
     int cstage = 0;
@@ -999,7 +1005,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       const Step cur = pend[0];
 #pragma unroll
       for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
-      pend[LA - 1] = next_step();
+      pend[LA - 1] = next_step(kind_c);
       const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
       fill_step(pend[LA - 1], fstage);
       const Slice s0 = make_slice(cur, cstage, 0);
@@ -1060,7 +1066,11 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // (every segment of a tile with correction steps takes the rescale,
     // so that their partials share one scale)
     walk_end = SEG ? min(s_hi, n_sel) : n_sel;
-    if (!SEG || walk_it < walk_end) run_walk(False{});
+    // (the two walks are instantiated for their kinds of steps, except with
+    // the D split, whose kernel measured 1 % slower with the second walk)
+    using KindExact = std::integral_constant<int, KSPLIT ? 0 : 1>;
+    using KindCorr = std::integral_constant<int, KSPLIT ? 0 : 2>;
+    if (!SEG || walk_it < walk_end) run_walk(False{}, KindExact{});
     if (n_corr > 0) {
       __syncthreads();  // every wave is done with the ring before it is refilled
 #pragma unroll
@@ -1071,10 +1081,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
       walk_it = SEG ? max(s_lo, n_sel) : n_sel;
       walk_end = s_hi;
-      if (!SEG || walk_it < walk_end) run_walk(False{});
+      if (!SEG || walk_it < walk_end) run_walk(False{}, KindCorr{});
     }
   } else {
-    run_walk(False{});
+    run_walk(False{}, std::integral_constant<int, 0>{});
   }
   row_sums();
   bool bad = false;
@@ -1114,7 +1124,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     walk_end = s_hi;
     start_windows(s_lo);
     load_cids(max(s_lo - n_sel, 0) * BN);
-    run_walk(True{});
+    run_walk(True{}, std::integral_constant<int, 0>{});
     row_sums();
   }
 
