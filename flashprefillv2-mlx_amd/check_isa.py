@@ -12,13 +12,13 @@ still in flight:
 
 * LDS operations (``ds_*``) complete in order; ``s_waitcnt lgkmcnt(N)``
   retires all but the N youngest;
-* the text is walked linearly, so instructions on skipped branch paths are
-  checked as if executed (conservative), and no read may stay in flight
-  across a backward branch (loop back-edge) or the end of a function (LDS
-  writes, which have no destination registers, still count towards the
-  in-order retirement but may stay in flight);
-* scalar-memory loads also count in lgkmcnt and may complete out of order; a
-  wait with N > 0 while such a load is outstanding retires no LDS read.
+* every path through the function's branches is followed (a dataflow over
+  its basic blocks, loops included), and no read may stay in flight at the
+  end of the function (LDS writes, which have no destination registers,
+  still count towards the in-order retirement but may stay in flight);
+* scalar-memory loads also count in lgkmcnt and may complete out of order,
+  but a wait for at most N outstanding operations in all leaves at most N
+  LDS operations outstanding, the N youngest, whatever else is in flight.
 
 Usage: ``python check_isa.py kernel.s [symbol-substring]``; exit status 1 on
 a violation.  ``build.py`` runs it on every build.
@@ -43,66 +43,110 @@ def _regs(operands: str) -> set[tuple[str, int]]:
     return out
 
 
-def check_function(name: str, lines: list[str]) -> list[str]:
-    errors: list[str] = []
-    pending: list[tuple[int, set]] = []  # in-flight LDS ops: (line, dest regs)
-    smem_outstanding = 0
-    labels: dict[str, int] = {}
-    for i, raw in enumerate(lines):
-        s = raw.split(";")[0].strip()
-        if not s:
-            continue
-        if s.endswith(":"):
-            labels[s[:-1]] = i
-            continue
-        if s.startswith("."):
-            continue
-        op, _, rest = s.partition(" ")
-        if op == "s_waitcnt":
-            m = _LGKM.search(rest)
-            if m:
-                n = int(m.group(1))
-                if n == 0:
-                    pending.clear()
-                    smem_outstanding = 0
-                elif smem_outstanding == 0:
-                    while len(pending) > n:
-                        pending.pop(0)
-            continue
-        if op.startswith("s_load") or op.startswith("s_buffer_load"):
-            smem_outstanding += 1
-        if op in ("s_branch", "s_cbranch_scc0", "s_cbranch_scc1", "s_cbranch_vccz",
-                  "s_cbranch_vccnz", "s_cbranch_execz", "s_cbranch_execnz"):
-            target = rest.strip()
-            if target in labels and any(d for _, d in pending):
-                errors.append(f"{name}: LDS read(s) from line(s) {[p[0] for p in pending if p[1]]} "
-                              f"in flight across the back-edge at line {i}: {s}")
-            continue
-        if op == "s_endpgm" and any(d for _, d in pending):
-            errors.append(f"{name}: LDS read(s) in flight at s_endpgm (line {i})")
-            continue
-        regs = _regs(rest)
-        if op.startswith("ds_"):
-            # operands: dest first for reads; a DS op may not touch in-flight dests either
-            dest: set = set()
-            if op.startswith("ds_read") or op.startswith("ds_bpermute") or op.startswith("ds_permute") \
-                    or op.startswith("ds_swizzle"):
-                first = rest.split(",")[0]
-                dest = _regs(first)
-                srcs = _regs(",".join(rest.split(",")[1:]))
-            else:
-                srcs = regs
-            for line_no, d in pending:
-                if (srcs | dest) & d:
-                    errors.append(f"{name}: line {i} `{s}` touches registers of the LDS "
-                                  f"read at line {line_no} before its wait")
-            pending.append((i, dest))
-            continue
+_BRANCHES = ("s_branch", "s_cbranch_scc0", "s_cbranch_scc1", "s_cbranch_vccz",
+             "s_cbranch_vccnz", "s_cbranch_execz", "s_cbranch_execnz")
+
+
+def _step(pending: tuple, op: str, rest: str, i: int, s: str, name: str, errors: list[str]):
+    """One instruction on one path's state: the tuple of in-flight LDS ops
+    ``(line, dest regs)``, oldest first.  Returns the state after it."""
+    if op == "s_waitcnt":
+        m = _LGKM.search(rest)
+        if m and len(pending) > int(m.group(1)):
+            n = int(m.group(1))
+            return pending[len(pending) - n:] if n else ()
+        return pending
+    regs = _regs(rest)
+    if op.startswith("ds_"):
+        # operands: dest first for reads; a DS op may not touch in-flight dests either
+        dest: frozenset = frozenset()
+        if op.startswith(("ds_read", "ds_bpermute", "ds_permute", "ds_swizzle")):
+            first = rest.split(",")[0]
+            dest = frozenset(_regs(first))
+            srcs = _regs(",".join(rest.split(",")[1:]))
+        else:
+            srcs = regs
         for line_no, d in pending:
-            if regs & d:
+            if (srcs | dest) & d:
                 errors.append(f"{name}: line {i} `{s}` touches registers of the LDS "
                               f"read at line {line_no} before its wait")
-    return errors
+        return pending + ((i, dest),)
+    for line_no, d in pending:
+        if regs & d:
+            errors.append(f"{name}: line {i} `{s}` touches registers of the LDS "
+                          f"read at line {line_no} before its wait")
+    return pending
+
+
+def check_function(name: str, lines: list[str]) -> list[str]:
+    """Dataflow over the function's basic blocks: each block's entry holds the
+    set of states of the paths that reach it (the fall-through and every
+    branch to its label, backward branches included), iterated until no
+    set grows."""
+    errors: list[str] = []
+    # basic blocks: (first line, [(line, op, rest, text)], successor labels, falls through)
+    blocks: list[tuple[str | None, list, list[str], bool]] = []
+    label: str | None = None
+    body: list = []
+
+    def close(succ: list[str], falls: bool) -> None:
+        nonlocal label, body
+        blocks.append((label, body, succ, falls))
+        label, body = None, []
+
+    for i, raw in enumerate(lines):
+        s = raw.split(";")[0].strip()
+        if not s or (s.startswith(".") and not s.endswith(":")):
+            continue
+        if s.endswith(":"):
+            close([], True)
+            label = s[:-1]
+            continue
+        op, _, rest = s.partition(" ")
+        if op in _BRANCHES:
+            close([rest.strip()], op != "s_branch")
+        elif op in ("s_endpgm", "s_setpc_b64"):
+            body.append((i, op, rest, s))
+            close([], False)
+        else:
+            body.append((i, op, rest, s))
+    close([], False)
+    index = {b[0]: k for k, b in enumerate(blocks) if b[0] is not None}
+
+    entry: list[set] = [set() for _ in blocks]
+    entry[0].add(())
+    work = [0]
+    while work:
+        k = work.pop()
+        _, body, succ, falls = blocks[k]
+        states = set(entry[k])
+        for i, op, rest, s in body:
+            if op == "s_endpgm":
+                if any(d for st in states for _, d in st):
+                    errors.append(f"{name}: LDS read(s) in flight at s_endpgm (line {i})")
+                continue
+            nxt = set()
+            for st in states:
+                st = _step(st, op, rest, i, s, name, errors)
+                if len(st) > 16:
+                    # an operation with no destination registers that 16
+                    # younger ones follow is retired by any wait (lgkmcnt
+                    # holds at most 15): drop it, so a loop's writes do not
+                    # grow the state
+                    st = tuple(p for k, p in enumerate(st) if p[1] or k >= len(st) - 16)
+                if len(st) > 64:
+                    errors.append(f"{name}: LDS reads accumulate without a wait (line {i})")
+                    st = st[-64:]
+                nxt.add(st)
+            states = nxt
+        targets = [index[t] for t in succ if t in index]
+        if falls and k + 1 < len(blocks):
+            targets.append(k + 1)
+        for t in targets:
+            if not states <= entry[t]:
+                entry[t] |= states
+                work.append(t)
+    return sorted(set(errors))
 
 
 def check_text(text: str, symbol_filter: str = "sparse_attn_kernel") -> list[str]:
