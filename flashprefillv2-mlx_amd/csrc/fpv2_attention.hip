@@ -140,10 +140,6 @@ struct AttnArgs {
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
-template <typename V>
-__device__ __forceinline__ V pick(bool c, V x, V y) {
-  return c ? x : y;
-}
 __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
@@ -461,14 +457,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     return ln;
   };
   // Byte offset of the lane's chunk relative to the sub-tile's first key
-  // (-1: a pad chunk past D).  Constant over the walk.
-  int pre[NI];
+  // (kOOB: a pad chunk past D).  Constant over the walk: an exact fill adds
+  // its sub-tile's offset as the instruction's scalar offset.
+  uint32_t pre[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int row = fill_row(i, lane);
     const int c = fill_chunk(i, row, lane);
     const int rs = i < NIK ? a.k_rs : a.v_rs;
-    pre[i] = c < GM::DG ? (row * rs + c * 8) * 2 : -1;
+    pre[i] = c < GM::DG ? static_cast<uint32_t>((row * rs + c * 8) * 2) : kOOB;
   }
   const uint32_t smem_lds = lds_addr(smem);
   // Correction fills take their pooled rows' block ids from cid: the
@@ -497,30 +494,48 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // (a lambda returning an LDS pointer would drop the kernel from the host
     // pass, so the destination is spelled out at each fill)
     uint8_t* const sp = smem + stage * GM::STAGE;
-    // (uniform: it selects the fills' buffer descriptors below)
+    // NI fills with per-lane offsets vo and the uniform offsets sk (K) and
+    // sv (V).  Each kind of step issues its own, so that the full exact
+    // fill, the common one, takes the constant offsets as they are.  (The
+    // builtin's arguments are plain locals: some argument expressions drop
+    // the kernel's host-side stub without a diagnostic.)
+    auto issue = [&](const uint32_t (&vo)[NI], uint32_t sk, uint32_t sv, rsrc_t rk, rsrc_t rv) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const rsrc_t r = i < NIK ? rk : rv;
+        const uint32_t o = vo[i];
+        const uint32_t so = i < NIK ? sk : sv;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024), 16, o, so,
+            0, 0);
+      }
+    };
+    // (uniform: it selects the kind of fill)
     const bool corr = CORR && __builtin_amdgcn_readfirstlane(s.corr) != 0;
-    uint32_t off[NI];
     if (!corr) {
+      // (uniform: the scalar offsets of the sub-tile's first key; a lane
+      // past the sub-tile's keys or past D has the offset kOOB, which
+      // stays out of range with them)
       const uint32_t kb = static_cast<uint32_t>(s.key0 * a.k_rs * 2);
       const uint32_t vb = static_cast<uint32_t>(s.key0 * a.v_rs * 2);
+      const rsrc_t rk = make_rsrc(kh, a.k_bytes);
+      const rsrc_t rv = make_rsrc(vh, a.v_bytes);
+      // (the empty asm statements that end the two paths differ, so the
+      // compiler does not merge their fills behind copies of the offsets)
       if (s.nkeys == BN) {  // full sub-tile
-#pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          bool ok = true;
-          if constexpr (GM::DG < GM::RC) ok = pre[i] >= 0;
-          off[i] = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
-        }
+        issue(pre, kb, vb, rk, rv);
+        asm volatile("; full sub-tile");
       } else {  // partial (end of the keys or of a block) or empty
         const int ln = opaque_lane();
+        uint32_t vo[NI];
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-          bool ok = fill_row(i, ln) < s.nkeys;
-          if constexpr (GM::DG < GM::RC) ok = ok && pre[i] >= 0;
-          off[i] = ok ? (i < NIK ? kb : vb) + static_cast<uint32_t>(pre[i]) : kOOB;
-        }
+        for (int i = 0; i < NI; ++i) vo[i] = fill_row(i, ln) < s.nkeys ? pre[i] : kOOB;
+        issue(vo, kb, vb, rk, rv);
+        asm volatile("; partial sub-tile");
       }
     } else {  // correction: pooled rows of the pruned blocks
       const int ln = opaque_lane();
+      uint32_t off[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int row = fill_row(i, ln);
@@ -529,21 +544,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
         const bool ok = row < s.nkeys && c < GM::DG;
         off[i] = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
       }
-    }
-    if (corr) load_cids(s.li + BN);  // the next correction step's entries
-    // (descriptors built from selected values: a select between two
-    // descriptors, or between two captured variables, is lowered through
-    // memory)
-    const rsrc_t rk = make_rsrc(pick(corr, pkh, kh), pick(corr, a.pooled_bytes, a.k_bytes));
-    const rsrc_t rv = make_rsrc(pick(corr, pvh, vh), pick(corr, a.pooled_bytes, a.v_bytes));
-    // (the builtin's arguments are plain locals: some argument expressions
-    // drop the kernel's host-side stub without a diagnostic)
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const rsrc_t r = i < NIK ? rk : rv;
-      const uint32_t o = off[i];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (lds_ptr)(sp + (i < NIK ? 0 : GM::TILE) + (wave + (i % NIK) * WAVES) * 1024), 16, o, 0, 0, 0);
+      load_cids(s.li + BN);  // the next correction step's entries
+      issue(off, 0u, 0u, make_rsrc(pkh, a.pooled_bytes), make_rsrc(pvh, a.pooled_bytes));
     }
   };
   // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
