@@ -140,6 +140,10 @@ struct AttnArgs {
 __device__ __forceinline__ void barrier_lds() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+template <typename V>
+__device__ __forceinline__ V pick(bool c, V x, V y) {
+  return c ? x : y;
+}
 __device__ __forceinline__ int clampi(int x, int lo, int hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
@@ -489,16 +493,15 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   };
   // (the first correction step of the workgroup's range)
   load_cids(max(s_lo - n_sel, 0) * BN);
-  auto fill_step = [&](const Step& s, int stage) {
+  auto fill_step = [&](const Step& s, int stage, auto kind_c) {
+    constexpr int KIND = decltype(kind_c)::value;
     typedef __attribute__((address_space(3))) void* lds_ptr;
     // (a lambda returning an LDS pointer would drop the kernel from the host
     // pass, so the destination is spelled out at each fill)
     uint8_t* const sp = smem + stage * GM::STAGE;
     // NI fills with per-lane offsets vo and the uniform offsets sk (K) and
-    // sv (V).  Each kind of step issues its own, so that the full exact
-    // fill, the common one, takes the constant offsets as they are.  (The
-    // builtin's arguments are plain locals: some argument expressions drop
-    // the kernel's host-side stub without a diagnostic.)
+    // sv (V).  (The builtin's arguments are plain locals: some argument
+    // expressions drop the kernel's host-side stub without a diagnostic.)
     auto issue = [&](const uint32_t (&vo)[NI], uint32_t sk, uint32_t sv, rsrc_t rk, rsrc_t rv) {
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -512,30 +515,13 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     };
     // (uniform: it selects the kind of fill)
     const bool corr = CORR && __builtin_amdgcn_readfirstlane(s.corr) != 0;
-    if (!corr) {
-      // (uniform: the scalar offsets of the sub-tile's first key; a lane
-      // past the sub-tile's keys or past D has the offset kOOB, which
-      // stays out of range with them)
-      const uint32_t kb = static_cast<uint32_t>(s.key0 * a.k_rs * 2);
-      const uint32_t vb = static_cast<uint32_t>(s.key0 * a.v_rs * 2);
-      const rsrc_t rk = make_rsrc(kh, a.k_bytes);
-      const rsrc_t rv = make_rsrc(vh, a.v_bytes);
-      // (the empty asm statements that end the two paths differ, so the
-      // compiler does not merge their fills behind copies of the offsets)
-      if (s.nkeys == BN) {  // full sub-tile
-        issue(pre, kb, vb, rk, rv);
-        asm volatile("; full sub-tile");
-      } else {  // partial (end of the keys or of a block) or empty
-        const int ln = opaque_lane();
-        uint32_t vo[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) vo[i] = fill_row(i, ln) < s.nkeys ? pre[i] : kOOB;
-        issue(vo, kb, vb, rk, rv);
-        asm volatile("; partial sub-tile");
-      }
-    } else {  // correction: pooled rows of the pruned blocks
+    // An exact fill takes its sub-tile's first key as the scalar offsets (a
+    // lane past the sub-tile's keys or past D has the offset kOOB, which
+    // stays out of range with them).
+    const uint32_t kb = static_cast<uint32_t>(s.key0 * a.k_rs * 2);
+    const uint32_t vb = static_cast<uint32_t>(s.key0 * a.v_rs * 2);
+    auto corr_offsets = [&](uint32_t (&off)[NI]) {  // pooled rows of the pruned blocks
       const int ln = opaque_lane();
-      uint32_t off[NI];
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int row = fill_row(i, ln);
@@ -544,8 +530,57 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
         const bool ok = row < s.nkeys && c < GM::DG;
         off[i] = ok ? static_cast<uint32_t>((blk * D + c * 8) * 2) : kOOB;
       }
-      load_cids(s.li + BN);  // the next correction step's entries
-      issue(off, 0u, 0u, make_rsrc(pkh, a.pooled_bytes), make_rsrc(pvh, a.pooled_bytes));
+    };
+    if constexpr (KIND != 0 || !CORR) {
+      // A walk of one kind of step: each kind of fill issues its own, so
+      // that the full exact fill, the common one, takes the constant
+      // offsets as they are.  (The empty asm statements that end the two
+      // exact paths differ, so the compiler does not merge their fills
+      // behind copies of the offsets.)
+      if (!corr) {
+        const rsrc_t rk = make_rsrc(kh, a.k_bytes);
+        const rsrc_t rv = make_rsrc(vh, a.v_bytes);
+        if (s.nkeys == BN) {  // full sub-tile
+          issue(pre, kb, vb, rk, rv);
+          asm volatile("; full sub-tile");
+        } else {  // partial (end of the keys or of a block) or empty
+          const int ln = opaque_lane();
+          uint32_t vo[NI];
+#pragma unroll
+          for (int i = 0; i < NI; ++i) vo[i] = fill_row(i, ln) < s.nkeys ? pre[i] : kOOB;
+          issue(vo, kb, vb, rk, rv);
+          asm volatile("; partial sub-tile");
+        }
+      } else {
+        uint32_t off[NI];
+        corr_offsets(off);
+        load_cids(s.li + BN);  // the next correction step's entries
+        issue(off, 0u, 0u, make_rsrc(pkh, a.pooled_bytes), make_rsrc(pvh, a.pooled_bytes));
+      }
+    } else {
+      // Both kinds in one walk: every fill is issued on one path after the
+      // next correction entries are loaded (see above).  Issued per kind,
+      // the entries' registers are copied at each exact step with a wait
+      // that covers the previous step's fills.
+      uint32_t vo[NI];
+      if (!corr) {
+        if (s.nkeys == BN) {
+#pragma unroll
+          for (int i = 0; i < NI; ++i) vo[i] = pre[i];
+        } else {
+          const int ln = opaque_lane();
+#pragma unroll
+          for (int i = 0; i < NI; ++i) vo[i] = fill_row(i, ln) < s.nkeys ? pre[i] : kOOB;
+        }
+      } else {
+        corr_offsets(vo);
+      }
+      if (corr) load_cids(s.li + BN);
+      // (descriptors built from selected values: a select between two
+      // descriptors, or between two captured variables, is lowered through
+      // memory)
+      issue(vo, corr ? 0u : kb, corr ? 0u : vb, make_rsrc(pick(corr, pkh, kh), pick(corr, a.pooled_bytes, a.k_bytes)),
+            make_rsrc(pick(corr, pvh, vh), pick(corr, a.pooled_bytes, a.v_bytes)));
     }
   };
   // Fills run LA = NST-2 sub-tiles ahead of the multiply, so that the stage
@@ -994,7 +1029,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
 #pragma unroll
     for (int p = 0; p < LA; ++p) {
       pend[p] = next_step(kind_c);
-      fill_step(pend[p], p);
+      fill_step(pend[p], p, kind_c);
     }
     int cstage = 0;
     // One sub-tile (one slice).  The pending slice enters in s_buf[P] and
@@ -1009,7 +1044,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
       pend[LA - 1] = next_step(kind_c);
       const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
-      fill_step(pend[LA - 1], fstage);
+      fill_step(pend[LA - 1], fstage, kind_c);
       const Slice s0 = make_slice(cur, cstage, 0);
       if constexpr (FIRST) process(True{}, False{}, NewB{}, MFirst{}, s0);
       else process(True{}, True{}, NewB{}, MRest{}, s0);
