@@ -649,6 +649,21 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   const int vm = GM::vmask(vrow);
   const uint32_t vbase = smem_lds + GM::TILE + (own + vrow) * ROWB + (((l16 & 3) >> 1) ^ vm) * 16 +
                          (l16 & 1) * 8 + dhalf * DT * 32;
+  // Walks whose ring stage is known at compile time (the 4-wave shape on
+  // whole tiles) read K and V at per-lane addresses computed once, with the
+  // stage in the instruction's immediate offset: the XOR terms touch
+  // address bits 4-7 only, which a stage offset (a multiple of the stage
+  // size) leaves alone.
+  constexpr bool kImm = !KSPLIT && !SEG;
+  static_assert(!kImm || (NST - 1) * GM::STAGE + 16 * ROWB < 65536, "ds offset field is 16 bits");
+  uint32_t kx[KSQ], vx[DT];
+  if constexpr (kImm) {
+#pragma unroll
+    for (int ks = 0; ks < KSQ; ++ks) kx[ks] = kbase ^ (64 * ks);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) vx[dt] = vbase ^ (32 * dt);
+  }
+  using NoStage = std::integral_constant<int, -1>;
 
   // ---- slice pipeline ----
   // A slice is 32 keys of a sub-tile.  Each slice passes two pipeline
@@ -705,12 +720,16 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   // contraction) and 16 + 4grp.. (slots 4-7), as the P words are ordered.
   // (DS = 2: slots 0-3 are the wave's own key tile, 16*dhalf + 4grp.., and
   // slots 4-7 the partner's, so the second read flips the 16-row offset.)
-  auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8]) {
+  auto issue_v = [&](uint32_t va, auto bc, u32x2 (&r)[8], auto sp_c) {
     constexpr int b = decltype(bc)::value;
+    constexpr int SP = decltype(sp_c)::value;  // the slice's stage, if known
     StaticFor<0, PER_BATCH>::run([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int dt = b * PER_BATCH + q;
-      if constexpr (dt < DT) {
+      if constexpr (dt < DT && kImm && SP >= 0) {
+        r[2 * q] = lds_read_tr<kAsm, SP * GM::STAGE>(vx[dt]);
+        r[2 * q + 1] = lds_read_tr<kAsm, SP * GM::STAGE + 16 * ROWB>(vx[dt]);
+      } else if constexpr (dt < DT) {
         const uint32_t addr = va ^ (32 * dt);
         r[2 * q] = lds_read_tr<kAsm, 0>(addr);
         if constexpr (KSPLIT) r[2 * q + 1] = lds_read_tr<kAsm, 0>(addr ^ (16 * ROWB));
@@ -731,7 +750,11 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   //   0  not computed (the fixed reference of the first pass),
   //   1  sets the reference (the first slice of the first pass),
   //   2  online reference with rescale (the exact pass).
-  auto process_m = [&](auto hn_c, auto hp_c, auto b_c, auto mask_c, auto mode_c, const Slice& nw) {
+  // SN, SP: the ring stages of the new and the pending slice when known at
+  // compile time (-1: from the slices' offsets).
+  auto process_m = [&](auto hn_c, auto hp_c, auto b_c, auto mask_c, auto mode_c, auto sn_c, auto sp_c,
+                       const Slice& nw) {
+    constexpr int SN = decltype(sn_c)::value;
     constexpr bool HN = decltype(hn_c)::value;
     constexpr bool HP = decltype(hp_c)::value;
     constexpr int B = decltype(b_c)::value;
@@ -756,6 +779,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       constexpr int i = decltype(ic)::value;
       constexpr int ks = i / 2, kt = i % 2;
       if constexpr (KSPLIT) return lds_read_b128<kAsm, 0>(ka ^ (64 * ks + kt * 16 * ROWB));
+      else if constexpr (kImm && SN >= 0) return lds_read_b128<kAsm, SN * GM::STAGE + kt * 16 * ROWB>(kx[ks]);
       else return lds_read_b128<kAsm, kt * 16 * ROWB>(ka ^ (64 * ks));
     };
 
@@ -782,7 +806,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
     }
     // V^T batch 0 after the first K window: those K reads do not wait behind it
-    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0]);
+    if constexpr (HP) issue_v(va, std::integral_constant<int, 0>{}, vb[0], sp_c);
     constexpr int NV0 = HP ? 2 * PER_BATCH : 0;  // reads of batch 0
     float bias[RT];
 #pragma unroll
@@ -920,7 +944,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       lgkm_wait<kAsm, 0>(vb[0]);
       StaticFor<0, BATCHES>::run([&](auto bc) {
         constexpr int b = decltype(bc)::value;
-        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1]);
+        if constexpr (b + 1 < BATCHES) issue_v(va, std::integral_constant<int, b + 1>{}, vb[(b + 1) & 1], sp_c);
         constexpr int NQ = (DT - b * PER_BATCH) < PER_BATCH ? (DT - b * PER_BATCH) : PER_BATCH;
         StaticFor<0, 2 * PER_BATCH>::run([&](auto qc) {
           constexpr int j = decltype(qc)::value;
@@ -1002,12 +1026,12 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   };
   // The mask decision is taken before the call so that stages A and B stay
   // free of branches.
-  auto process = [&](auto hn_c, auto hp_c, auto b_c, auto mode_c, const Slice& nw) {
+  auto process = [&](auto hn_c, auto hp_c, auto b_c, auto mode_c, const Slice& nw, auto sn_c, auto sp_c) {
     if constexpr (decltype(hn_c)::value) {
-      if (needs_mask(nw)) process_m(hn_c, hp_c, b_c, std::true_type{}, mode_c, nw);
-      else process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, nw);
+      if (needs_mask(nw)) process_m(hn_c, hp_c, b_c, std::true_type{}, mode_c, sn_c, sp_c, nw);
+      else process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, sn_c, sp_c, nw);
     } else {
-      process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, nw);
+      process_m(hn_c, hp_c, b_c, std::false_type{}, mode_c, sn_c, sp_c, nw);
     }
   };
 
@@ -1046,11 +1070,63 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       const int fstage = cstage >= 2 ? cstage - 2 : cstage + NST - 2;
       fill_step(pend[LA - 1], fstage, kind_c);
       const Slice s0 = make_slice(cur, cstage, 0);
-      if constexpr (FIRST) process(True{}, False{}, NewB{}, MFirst{}, s0);
-      else process(True{}, True{}, NewB{}, MRest{}, s0);
+      if constexpr (FIRST) process(True{}, False{}, NewB{}, MFirst{}, s0, NoStage{}, NoStage{});
+      else process(True{}, True{}, NewB{}, MRest{}, s0, NoStage{}, NoStage{});
       cstage = cstage == NST - 1 ? 0 : cstage + 1;
     };
-    if (count > 0) {
+    // The same with the ring stage known at compile time: sub-tile it is in
+    // stage it % NST, so NST sub-tiles per iteration (a multiple of the
+    // pending buffer's two).
+    auto do_step_at = [&](auto first_c, auto p_c, auto st_c) {
+      constexpr bool FIRST = decltype(first_c)::value;
+      constexpr int P = decltype(p_c)::value;
+      constexpr int ST = decltype(st_c)::value;
+      using NewB = std::integral_constant<int, 1 - P>;
+      using SP = std::integral_constant<int, (ST + NST - 1) % NST>;
+      fills_done();
+      const Step cur = pend[0];
+#pragma unroll
+      for (int p = 0; p < LA - 1; ++p) pend[p] = pend[p + 1];
+      pend[LA - 1] = next_step(kind_c);
+      fill_step(pend[LA - 1], (ST + LA) % NST, kind_c);
+      const Slice s0 = make_slice(cur, ST, 0);
+      if constexpr (FIRST) process(True{}, False{}, NewB{}, MFirst{}, s0, st_c, NoStage{});
+      else process(True{}, True{}, NewB{}, MRest{}, s0, st_c, SP{});
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1 % NST>;
+    using S2 = std::integral_constant<int, 2 % NST>;
+    using S3 = std::integral_constant<int, 3 % NST>;
+    // (exact walks only: in the correction and online walks the per-lane
+    // addresses would stay live beside their own registers and spill)
+    if constexpr (kImm && NST == 4 && decltype(kind_c)::value == 1) {
+      if (count > 0) {
+        do_step_at(True{}, P0{}, S0{});
+        int it = 1;
+        for (; it + 3 < count; it += 4) {
+          do_step_at(False{}, P1{}, S1{});
+          do_step_at(False{}, P0{}, S2{});
+          do_step_at(False{}, P1{}, S3{});
+          do_step_at(False{}, P0{}, S0{});
+        }
+        if (it < count) {
+          do_step_at(False{}, P1{}, S1{});
+          if (it + 1 < count) {
+            do_step_at(False{}, P0{}, S2{});
+            if (it + 2 < count) {
+              do_step_at(False{}, P1{}, S3{});
+              process(False{}, True{}, P1{}, MRest{}, p_pend, NoStage{}, S3{});
+            } else {
+              process(False{}, True{}, P0{}, MRest{}, p_pend, NoStage{}, S2{});
+            }
+          } else {
+            process(False{}, True{}, P1{}, MRest{}, p_pend, NoStage{}, S1{});
+          }
+        } else {
+          process(False{}, True{}, P0{}, MRest{}, p_pend, NoStage{}, S0{});
+        }
+      }
+    } else if (count > 0) {
       do_step(True{}, P0{});  // the first sub-tile has no pending slice
       // the pending buffer alternates, so two sub-tiles per iteration
       int it = 1;
@@ -1060,9 +1136,9 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
       if (it < count) {
         do_step(False{}, P1{});
-        process(False{}, True{}, P1{}, MRest{}, p_pend);  // pending in s_buf[0]
+        process(False{}, True{}, P1{}, MRest{}, p_pend, NoStage{}, NoStage{});  // pending in s_buf[0]
       } else {
-        process(False{}, True{}, P0{}, MRest{}, p_pend);  // pending in s_buf[1]
+        process(False{}, True{}, P0{}, MRest{}, p_pend, NoStage{}, NoStage{});  // pending in s_buf[1]
       }
     }
     // No fill may land in LDS after the walk ends.
