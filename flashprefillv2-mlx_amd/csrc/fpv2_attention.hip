@@ -1197,7 +1197,8 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       if (!SEG || walk_it < walk_end) run_walk(False{}, KindCorr{});
     }
   } else {
-    run_walk(False{}, std::integral_constant<int, 0>{});
+    // (without correction every step is exact)
+    run_walk(False{}, std::integral_constant<int, CORR ? 0 : 1>{});
   }
   row_sums();
   bool bad = false;
