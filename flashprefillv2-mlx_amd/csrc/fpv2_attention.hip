@@ -1043,10 +1043,11 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
   using False = std::integral_constant<bool, false>;
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  auto run_walk = [&](auto online_c, auto kind_c) {
+  // cont_c: the walk continues an earlier walk's fixed reference.
+  auto run_walk = [&](auto online_c, auto kind_c, auto cont_c) {
     constexpr bool ONLINE = decltype(online_c)::value;
     // (the reference-free pass computes no row max, not even for the first slice)
-    using MFirst = std::integral_constant<int, ONLINE ? 2 : (kFree ? 0 : 1)>;
+    using MFirst = std::integral_constant<int, ONLINE ? 2 : ((kFree || decltype(cont_c)::value) ? 0 : 1)>;
     using MRest = std::integral_constant<int, ONLINE ? 2 : 0>;
     const int count = walk_end - walk_it;  // sub-tiles of this walk
     Step pend[LA];
@@ -1183,7 +1184,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     // the D split, whose kernel measured 1 % slower with the second walk)
     using KindExact = std::integral_constant<int, KSPLIT ? 0 : 1>;
     using KindCorr = std::integral_constant<int, KSPLIT ? 0 : 2>;
-    if (!SEG || walk_it < walk_end) run_walk(False{}, KindExact{});
+    if (!SEG || walk_it < walk_end) run_walk(False{}, KindExact{}, False{});
     if (n_corr > 0) {
       __syncthreads();  // every wave is done with the ring before it is refilled
 #pragma unroll
@@ -1194,11 +1195,23 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
       }
       walk_it = SEG ? max(s_lo, n_sel) : n_sel;
       walk_end = s_hi;
-      if (!SEG || walk_it < walk_end) run_walk(False{}, KindCorr{});
+      if (!SEG || walk_it < walk_end) run_walk(False{}, KindCorr{}, False{});
+    }
+  } else if constexpr (CORR && !SEG && !KSPLIT) {
+    // float16 with correction: the exact steps, then the correction steps,
+    // whose slices keep the reference the first exact slice fixed (every
+    // tile selects a block: the largest energy passes any alpha <= 1).
+    walk_end = n_sel;
+    run_walk(False{}, std::integral_constant<int, 1>{}, False{});
+    if (n_corr > 0) {
+      __syncthreads();  // every wave is done with the ring before it is refilled
+      walk_it = n_sel;
+      walk_end = s_hi;
+      run_walk(False{}, std::integral_constant<int, 2>{}, True{});
     }
   } else {
     // (without correction every step is exact)
-    run_walk(False{}, std::integral_constant<int, CORR ? 0 : 1>{});
+    run_walk(False{}, std::integral_constant<int, CORR ? 0 : 1>{}, False{});
   }
   row_sums();
   bool bad = false;
@@ -1238,7 +1251,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     walk_end = s_hi;
     start_windows(s_lo);
     load_cids(max(s_lo - n_sel, 0) * BN);
-    run_walk(True{}, std::integral_constant<int, 0>{});
+    run_walk(True{}, std::integral_constant<int, 0>{}, False{});
     row_sums();
   }
 
