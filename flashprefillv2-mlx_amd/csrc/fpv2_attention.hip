@@ -1199,8 +1199,10 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     }
   } else if constexpr (CORR && !SEG && !KSPLIT) {
     // float16 with correction: the exact steps, then the correction steps,
-    // whose slices keep the reference the first exact slice fixed (every
-    // tile selects a block: the largest energy passes any alpha <= 1).
+    // whose slices keep the reference the first exact slice fixed.  (A
+    // tile of the hook always selects a block, the largest energy passing
+    // any alpha <= 1; a tile whose lists, given through the C ABI, select
+    // none has no fixed reference and takes the online walk below.)
     walk_end = n_sel;
     run_walk(False{}, std::integral_constant<int, 1>{}, False{});
     if (n_corr > 0) {
@@ -1226,6 +1228,7 @@ __global__ __launch_bounds__(WAVES * 64, ((D <= 128 || DS == 2) ? 2 : 1)) void s
     const float l = l_tot[rt];
     bad = bad || (row_valid[rt] && !(l >= 0x1p-60f && l <= 0x1p64f && fin));
   }
+  if constexpr (CORR && !kFree && !SEG && !KSPLIT) bad = bad || n_sel == 0;  // (see the walks above)
   // Workgroup-wide decision through the last ring stage, which the second
   // walk refills only after its first barrier (the flags are read by then).
   int* const flags = reinterpret_cast<int*>(smem + (NST - 1) * GM::STAGE);

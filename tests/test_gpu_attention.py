@@ -320,6 +320,45 @@ def test_crafted_lists_at_window_and_correction_boundaries(cuda, head_dim):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_tiles_selecting_no_block_use_only_the_pooled_rows(cuda, dtype, head_dim):
+    # lists given through the operator may select nothing for a tile (the
+    # hook never does: the largest energy passes any alpha <= 1); its rows
+    # then attend to the pooled rows of the pruned blocks alone, with no
+    # exact slice to fix a reference (float16 takes the online walk)
+    config = FPV2Config(block_k=32, tile_q=32, alpha=0.1, mean_correction=True)
+    length, hq, hkv = 2048, 4, 1
+    nt = nb = length // 32
+    g = torch.Generator().manual_seed(83)
+    q, k, v = structured_qkv(length=length, query_heads=hq, kv_heads=hkv, head_dim=head_dim,
+                             block_size=32, seed=83)
+    selected = torch.rand((hkv, nt, nb), generator=g) < 0.3
+    selected &= torch.arange(nb)[None, None, :] <= torch.arange(nt)[None, :, None]  # causal
+    selected[:, torch.arange(nt), torch.arange(nt)] = True  # the diagonal block
+    empty = (3, 17, 40, nt - 1)
+    for t in empty:
+        selected[:, t] = False
+    qd, kd, vd = (x.to(dtype).to(cuda) for x in (q, k, v))
+    pk = pool_blocks(kd, config.block_k)
+    pv = pool_blocks(vd, config.block_k)
+    lists = compact_block_indices(selected.to(cuda), config=config, query_length=length, key_length=length)
+    counts, pcounts = lists[1].cpu(), lists[3].cpu()
+    for t in empty:
+        assert int(counts[0, t]) == 0 and int(pcounts[0, t]) == t
+    out = sparse_attention(qd, kd, vd, pk, pv, *lists, scale=head_dim ** -0.5, config=config)
+    torch.cuda.synchronize()
+    qn, kn, vn = (to_np(x.to(dtype)) for x in (q, k, v))
+    ref = orc.fpv2_attention_blockwise(qn, kn, vn, scale=head_dim ** -0.5, selected=selected.numpy(),
+                                       pooled_k=to_np(pk), pooled_v=to_np(pv), config=_cfg(config))
+    got = to_np(out)
+    err = attention_errors(got, ref)
+    assert err["max_abs"] <= MAX_ABS and err["mean_abs"] <= MEAN_ABS, err
+    rows = np.concatenate([np.arange(t * 32, (t + 1) * 32) for t in empty])
+    err_empty = attention_errors(got[:, rows], ref[:, rows])
+    assert err_empty["max_abs"] <= MAX_ABS and err_empty["mean_abs"] <= MEAN_ABS, err_empty
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_head_dim_256_reruns_are_bitwise_identical(cuda, dtype):
     """head_dim 256 exchanges partial logits, P and row statistics between
     the two waves of each row group through LDS: repeated launches on the
